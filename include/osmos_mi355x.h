@@ -1,0 +1,51 @@
+/* libosmos MI355X - entry points of this library that have no single counterpart in the reference's kernel ABI:
+   the device-side version of the lane's host table build and the whole routed layer it feeds. everything else this
+   library exports is declared, signature for signature, in include/osmos/gpu/{q8,mv,mmq,quant,q4x_ops,ops}.h. */
+#ifndef OSMOS_MI355X_H
+#define OSMOS_MI355X_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#include "osmos/gpu/mmq.h"
+#include "osmos/gpu/mv.h"
+#include "osmos/gpu/ops.h"
+#include "osmos/gpu/q4x_ops.h"
+#include "osmos/gpu/q8.h"
+#include "osmos/gpu/quant.h"
+
+#define OSMOS_LANE_MAX_PAIRS 4096 /* osmos_lane_tables' most (token, expert) pairs a step */
+
+/* the lane's tables for one step, on the device (what reference src/run/hip_lane.c:115-200 builds on the host after
+   copying the picks back; here no host round trip): the step's n_tok x k picks `ids` sorted by (expert, pick) into pair
+   rows r; tok[r] the pair's token, pair[r] its pick index (t k + j); entries of at most MV_MAX_TOKENS rows of one
+   expert (an expert's rows split in order), entry e: cnt[e], xrow[e] (its first pair row) and its three matrices
+   wg/wu/wd[e] = base[i] + expert * bytes[i]; entries past the live ones cnt 0 up to n_tok k; order[t k + j] token t's
+   pair rows in ascending row (= ascending expert id), for ops_gather_sum_add. all outputs device memory of n_tok k
+   entries. false, nothing queued, for n_tok k past OSMOS_LANE_MAX_PAIRS, k 0, n_exp 0, or a launch refused. */
+bool osmos_lane_tables(const int32_t *ids, uint32_t n_tok, uint32_t k, uint32_t n_exp, const void *const *base,
+                       const uint64_t *bytes, int32_t *tok, int32_t *pair, int32_t *cnt, int32_t *xrow,
+                       const void **wg, const void **wu, const void **wd, int32_t *order, void *stream);
+
+/* one routed MoE layer over the lane's int8 contract, on the device, as the reference's lane runs it
+   (src/run/hip_lane.c:115-222 with the tables of osmos_lane_tables, src/cpu/lane.c:98-118's phases): x's n_tok rows
+   rounded (q8_round), each expert's gate and up with the activation lane_swiglu(g, u, lim, w[pick]) (q8_gate_up, inputs
+   by token, weights by pick), the activations rounded, down (q8_group_tok), then each token's expert rows summed in
+   ascending expert id and add[t] added after (ops_gather_sum_add) into out (n_tok rows of dim). the bits of the
+   reference CPU lane for every token, whatever n_tok. `gate`, `up`, `down`: each tensor's n_exp experts back to back,
+   an expert `*_bytes` apart (GGUF rows: gate/up ff rows of dim, down dim rows of ff); ids / w: the router's n_tok x k
+   picks and weights. workspace: device memory of osmos_lane_workspace bytes (256-aligned), the caller's. */
+typedef struct OsmosLaneLayer
+{
+  uint32_t type_gu, type_down; /* the lane's types (q8.h) */
+  uint32_t dim, ff, n_exp, k;
+  float lim;                   /* the activation's clamp (INFINITY: none) */
+  const void *gate, *up, *down;
+  uint64_t gate_bytes, up_bytes, down_bytes;
+} OsmosLaneLayer;
+
+uint64_t osmos_lane_workspace(const OsmosLaneLayer *layer, uint32_t n_tok);
+bool osmos_lane_layer(const OsmosLaneLayer *layer, const float *x, uint32_t n_tok, const int32_t *ids, const float *w,
+                      const float *add, float *out, void *workspace, uint64_t workspace_bytes, void *stream);
+
+#endif

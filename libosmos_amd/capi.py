@@ -1,0 +1,92 @@
+"""ctypes bindings of libosmos_mi355x.so's C ABI (the declarations in include/osmos/gpu/*.h and
+include/osmos_mi355x.h), argument for argument: pointers are device addresses (a torch tensor's data_ptr() or a
+hipMalloc'd address), `stream` a hipStream_t (torch.cuda.current_stream().cuda_stream) or None for the default.
+
+the library is never replaced by anything else: if libosmos_mi355x.so is missing, lib() raises - there is no CPU
+fallback on the product path.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libosmos_mi355x.so")
+
+P = ctypes.c_void_p
+U32 = ctypes.c_uint32
+U64 = ctypes.c_uint64
+F32 = ctypes.c_float
+B = ctypes.c_bool
+
+# name -> (restype, argtypes); the exact C signatures
+SIGS = {
+    "q8_round": (B, [P, U32, U32, U32, P, P, P]),
+    "q8_group_tok": (B, [U32, P, P, P, P, U32, U32, U32, U32, P, P, P, U32, P]),
+    "q8_gate_up": (B, [U32, P, P, P, P, P, P, U32, U32, U32, U32, P, P, P, F32, P, U32, P]),
+    "mv_run": (B, [U32, P, U32, U32, P, U32, P, P]),
+    "mv_group": (B, [U32, P, U32, U32, U32, P, U32, U32, P, P]),
+    "mv_group_tok": (B, [U32, P, P, P, U32, U32, U32, U32, P, U32, P, U32, P]),
+    "mv_strided": (B, [U32, P, U32, U32, P, U32, U32, P, U32, P]),
+    "quant_known": (B, [U32]),
+    "mmq_known": (B, [U32]),
+    "mmq_x8_rows": (B, [P, U32, P, U32, U32, P, P, P, P]),
+    "mmq_group": (B, [U32, P, P, U32, U32, U32, U32, P, P, P, P, P, P, U32, P]),
+    "q4x_route": (B, [P, U32, U32, U32, P, P, P, P]),
+    "q4x_expert_bounds": (None, [U32, U32, P]),
+    "q4x_expert_tiles": (B, [P, U32, U32, U32, U32, U32, P, P]),
+    "q4x_moe_sum": (B, [P, P, P, U32, U32, U32, P, P, P, P]),
+    "ops_swiglu_lane": (B, [P, P, U32, F32, P, U32, P, P]),
+    "ops_gather_rows": (B, [P, P, P, U32, U32, P]),
+    "ops_gather_sum_add": (B, [P, P, P, U32, U32, U32, P, P]),
+    "osmos_lane_tables": (B, [P, U32, U32, U32, P, P, P, P, P, P, P, P, P, P, P]),
+    "quant_dequant": (B, [U32, P, U64, P, P]),
+}
+
+
+
+class OsmosLaneLayer(ctypes.Structure):
+    """include/osmos_mi355x.h's OsmosLaneLayer"""
+    _fields_ = [("type_gu", U32), ("type_down", U32), ("dim", U32), ("ff", U32), ("n_exp", U32), ("k", U32),
+                ("lim", F32), ("gate", P), ("up", P), ("down", P), ("gate_bytes", U64), ("up_bytes", U64),
+                ("down_bytes", U64)]
+
+
+class Q4xExpertTiles(ctypes.Structure):
+    """include/osmos/gpu/q4x_ops.h's Q4xExpertTiles"""
+    _fields_ = [("base", P * 3), ("bytes", U64 * 3), ("tab", P * 3), ("ptr", P * 3), ("cnt", P), ("gidx", P),
+                ("hidx", P), ("xg", P), ("yg", P), ("xd", P), ("yd", P), ("where", P), ("off", P)]
+
+
+class Q4xExpertBounds(ctypes.Structure):
+    _fields_ = [("first", U32 * 4), ("count", U32 * 4), ("entries", U32), ("slots", U32)]
+
+
+SIGS.update({
+    "osmos_lane_workspace": (U64, [ctypes.POINTER(OsmosLaneLayer), U32]),
+    "osmos_lane_layer": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P, P, U64, P]),
+})
+
+_lib = None
+
+
+class MissingLibrary(RuntimeError):
+    pass
+
+
+def lib():
+    """the loaded library (built by `python -m libosmos_amd.build` or __graft_entry__.build())"""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MissingLibrary("%s is not built: run python -m libosmos_amd.build (no fallback exists)" % LIB_PATH)
+        h = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGS.items():
+            if hasattr(h, name):
+                f = getattr(h, name)
+                f.restype, f.argtypes = res, args
+        _lib = h
+    return _lib
+
+
+def addr(t):
+    """a tensor's device address (None for None)"""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())

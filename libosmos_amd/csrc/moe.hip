@@ -1,0 +1,369 @@
+// libosmos MI355X - the MoE plumbing around the expert products: the Qwen-style routing, expert tables and weighted
+// sum (include/osmos/gpu/q4x_ops.h), the lane's element-wise ops (include/osmos/gpu/ops.h) and the lane's step tables
+// built on the device (include/osmos_mi355x.h: osmos_lane_tables).
+//
+// contracts: reference include/osmos/gpu/q4x_ops.h:356-384 and kernels/q4x_moe.hip:38-200 (route: softmax, the k
+// greatest, the lowest id among equals, weights over max(sum, 6.103515625e-5); tiles: picks sorted by expert then pick,
+// slots in whole tiles of 16, parts of at most 128 tokens in runs of 1/2/4/8 tiles; the sum: picks in order, then the
+// sigmoid-gated shared expert), reference include/osmos/gpu/ops.h:311-355 and kernels/ops.hip:502-525 (swiglu_lane,
+// gather_rows, gather_sum_add), reference src/run/hip_lane.c:115-200 (the lane's entries and token order).
+#include "common.h"
+
+extern "C" {
+#include "../../include/osmos_mi355x.h"
+}
+
+namespace osm {
+namespace moe {
+
+constexpr uint32_t kMaxExperts = 1024, kMaxK = 32;
+constexpr float kSumFloor = 6.103515625e-5f;
+constexpr int kTile = 16, kPart = kTile << (Q4X_TILE_RUNS - 1);  // 128: an entry's most tokens
+
+__device__ inline float pick_key(float x) { return x == x ? x : -__builtin_inff(); }
+__device__ inline float sigmoid(float x) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x))); }
+
+// ---- q4x_route: a workgroup a token; the softmax by workgroup trees, the picks by its first wave ----
+constexpr int kRouteThreads = 256, kRouteLane = kMaxExperts / kWave;
+
+__device__ inline float wg_reduce(float v, float* lds, bool is_max) {
+  lds[threadIdx.x] = v;
+  __syncthreads();
+  for (int s = kRouteThreads / 2; s > 0; s >>= 1) {
+    if ((int) threadIdx.x < s)
+      lds[threadIdx.x] = is_max ? fmaxf(lds[threadIdx.x], lds[threadIdx.x + s]) : __fadd_rn(lds[threadIdx.x], lds[threadIdx.x + s]);
+    __syncthreads();
+  }
+  const float r = lds[0];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* __restrict__ logits, uint32_t n_exp,
+                                                              uint32_t k, int32_t* __restrict__ ids,
+                                                              float* __restrict__ w, int32_t* __restrict__ rows) {
+  __shared__ float p[kMaxExperts], lds[kRouteThreads];
+  const uint32_t t = blockIdx.x;
+  const float* l = logits + (uint64_t) t * n_exp;
+  float m = -__builtin_inff();
+  for (uint32_t i = threadIdx.x; i < n_exp; i += kRouteThreads) m = fmaxf(m, l[i]);
+  m = wg_reduce(m, lds, true);
+  float sum = 0.0f;
+  for (uint32_t i = threadIdx.x; i < n_exp; i += kRouteThreads) sum = __fadd_rn(sum, (p[i] = expf(__fsub_rn(l[i], m))));
+  const float inv = __fdiv_rn(1.0f, wg_reduce(sum, lds, false));
+  for (uint32_t i = threadIdx.x; i < n_exp; i += kRouteThreads) p[i] = __fmul_rn(p[i], inv);
+  __syncthreads();
+  if (threadIdx.x >= kWave) return;
+  const uint32_t lane = threadIdx.x;
+  float v[kRouteLane];
+  for (int r = 0; r < kRouteLane; r++) v[r] = lane + kWave * r < n_exp ? pick_key(p[lane + kWave * r]) : -__builtin_inff();
+  uint32_t taken = 0;
+  float pick[kMaxK], total = 0.0f;
+  for (uint32_t j = 0; j < k; j++) {
+    float bv = -__builtin_inff();
+    int bi = INT32_MAX;
+    for (int r = 0; r < kRouteLane; r++) {  // ascending ids within the lane: a strict > keeps the lowest
+      const uint32_t e = lane + kWave * r;
+      if (e < n_exp && !(taken >> r & 1) && (bi == INT32_MAX || v[r] > bv)) bv = v[r], bi = (int) e;
+    }
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, kWave);
+      const int oi = __shfl_xor(bi, o, kWave);
+      if (oi != INT32_MAX && (bi == INT32_MAX || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
+    }
+    if ((uint32_t) bi % kWave == lane) taken |= 1u << ((uint32_t) bi / kWave);
+    pick[j] = bv, total = __fadd_rn(total, bv);
+    if (!lane) ids[t * k + j] = bi, rows[t * k + j] = (int32_t) t;
+  }
+  if (lane) return;
+  const float div = fmaxf(total, kSumFloor);
+  for (uint32_t j = 0; j < k; j++) w[t * k + j] = __fdiv_rn(pick[j], div);
+}
+
+// ---- q4x_expert_tiles ----
+__device__ inline int run_of(int c) { return c <= 16 ? 0 : c <= 32 ? 1 : c <= 64 ? 2 : 3; }
+
+constexpr int kTileThreads = 1024, kScans = 2 + Q4X_TILE_RUNS;  // places, slots, each run's entries
+constexpr uint32_t kPlaceInline = 256;
+
+// expert e's own share of scan a: its picks, its slots (whole tiles), its entries in run r
+__device__ inline int own(int c, int a) {
+  if (a == 0) return c;
+  if (a == 1) return (c + kTile - 1) / kTile * kTile;
+  const int r = a - 2, rem = c % kPart;
+  return (r == Q4X_TILE_RUNS - 1 ? c / kPart : 0) + (rem && run_of(rem) == r);
+}
+
+__global__ __launch_bounds__(kTileThreads) void tiles_kernel(const int32_t* __restrict__ ids, uint32_t n, uint32_t k,
+                                                             uint32_t n_exp, uint32_t dim, uint32_t ff,
+                                                             Q4xExpertTiles t, Q4xExpertBounds bd) {
+  __shared__ int count[kMaxExperts], sc[kScans][kMaxExperts], total[kScans];
+  const uint32_t e = threadIdx.x;  // a thread an expert (n_exp <= 1024)
+  if (e < n_exp) count[e] = 0;
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < n; i += kTileThreads) atomicAdd(&count[ids[i]], 1);
+  __syncthreads();
+  const int c = e < n_exp ? count[e] : 0;
+  for (int a = 0; a < kScans; a++) sc[a][e] = e < n_exp ? own(c, a) : 0;
+  __syncthreads();
+  for (uint32_t d = 1; d < kMaxExperts; d <<= 1) {  // inclusive scans (Hillis-Steele) over the 1024 places
+    int v[kScans];
+    for (int a = 0; a < kScans; a++) v[a] = e >= d ? sc[a][e - d] : 0;
+    __syncthreads();
+    for (int a = 0; a < kScans; a++) sc[a][e] += v[a];
+    __syncthreads();
+  }
+  if (threadIdx.x < (uint32_t) kScans) total[threadIdx.x] = sc[threadIdx.x][kMaxExperts - 1];
+  __syncthreads();
+  if (e < n_exp) {
+    int ex[kScans];
+    for (int a = 0; a < kScans; a++) ex[a] = sc[a][e] - own(c, a);
+    t.off[e] = ex[0], t.off[n_exp + e] = ex[1], t.off[2 * n_exp + e] = c;
+    if (c) {
+      const int p0 = ex[0], s0 = ex[1];
+      if (n <= kPlaceInline) {  // this expert's picks in pick order
+        int q = p0;
+        for (uint32_t i = 0; i < n && q < p0 + c; i++)
+          if (ids[i] == (int32_t) e) t.where[i] = q, t.gidx[s0 + q - p0] = (int32_t) (i / k), t.hidx[s0 + q - p0] = q, q++;
+      }
+      for (int s = s0 + c; s < s0 + own(c, 1); s++) t.gidx[s] = -1, t.hidx[s] = -1;
+      int at[Q4X_TILE_RUNS];
+      for (int r = 0; r < Q4X_TILE_RUNS; r++) at[r] = (int) bd.first[r] + ex[2 + r];
+      for (int part = 0; part * kPart < c; part++) {
+        const int m = c - part * kPart < kPart ? c - part * kPart : kPart, en = at[run_of(m)]++;
+        const int slot = s0 + part * kPart, place = p0 + part * kPart;
+        t.cnt[en] = m;
+        t.xg[en] = (uint32_t) slot * dim, t.xd[en] = (uint32_t) slot * ff;
+        t.yg[en] = (uint32_t) place * ff, t.yd[en] = (uint32_t) place * dim;
+        for (int j = 0; j < Q4X_GROUP_TENSORS; j++)
+          t.ptr[j][en] = t.tab[j] ? t.tab[j][e] : (const uint8_t*) t.base[j] + (uint64_t) e * t.bytes[j];
+      }
+    }
+  }
+  for (int r = 0; r < Q4X_TILE_RUNS; r++)
+    for (uint32_t i = (uint32_t) total[2 + r] + threadIdx.x; i < bd.count[r]; i += kTileThreads) t.cnt[bd.first[r] + i] = 0;
+  for (uint32_t s = (uint32_t) total[1] + threadIdx.x; s < bd.slots; s += kTileThreads) t.gidx[s] = -1, t.hidx[s] = -1;
+}
+
+// a workgroup an expert: its picks placed in pick order, a tile of 256 picks at a time (a wave's ballot prefix, then
+// the waves' counts in order)
+constexpr int kPlaceThreads = 256;
+__global__ __launch_bounds__(kPlaceThreads) void place_kernel(const int32_t* __restrict__ ids, uint32_t n, uint32_t k,
+                                                              uint32_t n_exp, Q4xExpertTiles t) {
+  __shared__ int wave_cnt[kPlaceThreads / kWave];
+  const uint32_t e = blockIdx.x;
+  const int c = t.off[2 * n_exp + e];
+  if (!c) return;
+  const int p0 = t.off[e], s0 = t.off[n_exp + e];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  int done = 0;
+  for (uint32_t i0 = 0; i0 < n && done < c; i0 += kPlaceThreads) {
+    const uint32_t i = i0 + threadIdx.x;
+    const bool f = i < n && ids[i] == (int32_t) e;
+    const uint64_t mask = __ballot(f);
+    const int before = __builtin_popcountll(mask & ((1ull << lane) - 1));
+    if (lane == 0) wave_cnt[wave] = __builtin_popcountll(mask);
+    __syncthreads();
+    int base = done;
+    for (int v = 0; v < wave; v++) base += wave_cnt[v];
+    if (f) {
+      const int q = p0 + base + before;
+      t.where[i] = q, t.gidx[s0 + q - p0] = (int32_t) (i / k), t.hidx[s0 + q - p0] = q;
+    }
+    for (int v = 0; v < kPlaceThreads / kWave; v++) done += wave_cnt[v];
+    __syncthreads();
+  }
+}
+
+// ---- q4x_moe_sum (kernels/q4x_moe.hip:172-180): each value its own products and sums, in pick order ----
+__global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ y, const int32_t* __restrict__ where,
+                                                      const float* __restrict__ w, uint32_t n_tok, uint32_t k,
+                                                      uint32_t dim, const float* __restrict__ shared,
+                                                      const float* __restrict__ shared_logit, float* __restrict__ out) {
+  const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t) n_tok * dim) return;
+  const uint64_t t = i / dim, d = i % dim;
+  float sum = 0.0f;
+  for (uint32_t j = 0; j < k; j++) sum = __fadd_rn(sum, __fmul_rn(y[(uint64_t) where[t * k + j] * dim + d], w[t * k + j]));
+  out[i] = __fadd_rn(sum, __fmul_rn(shared[i], sigmoid(shared_logit[t])));
+}
+
+// ---- ops ----
+__global__ __launch_bounds__(256) void swiglu_lane_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          uint32_t n, float lim, const float* __restrict__ scale,
+                                                          uint32_t n_tok, float* __restrict__ h) {
+  const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t) n * n_tok) return;
+  h[i] = lane_swiglu(g[i], u[i], lim, scale[i / n]);
+}
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                          const int32_t* __restrict__ idx, uint32_t n, uint32_t len) {
+  const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
+  if (i < (uint64_t) n * len) dst[i] = src[(uint64_t) idx[i / len] * len + i % len];
+}
+
+// y[t][d] = sum over j in order of src[idx[t m + j]][d] (from 0), then add's (kernels/ops.hip:515-525); 4 values a thread
+__global__ __launch_bounds__(256) void gather_sum_kernel(float* __restrict__ y, const float* __restrict__ src,
+                                                         const int32_t* __restrict__ idx, uint32_t m, uint32_t n,
+                                                         uint32_t dim, const float* __restrict__ add) {
+  const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t) n * dim) return;
+  const uint32_t t = (uint32_t) (i / dim), d = (uint32_t) (i % dim);
+  float s = 0.0f;
+  for (uint32_t j = 0; j < m; j++) s = __fadd_rn(s, src[(uint64_t) idx[t * m + j] * dim + d]);
+  y[i] = add ? __fadd_rn(s, add[i]) : s;
+}
+
+// ---- osmos_lane_tables: the lane's step tables on the device (reference src/run/hip_lane.c:115-200's) ----
+constexpr int kLaneThreads = 1024;
+struct LaneBases {
+  const uint8_t* base[3];
+  uint64_t bytes[3];
+};
+
+__global__ __launch_bounds__(kLaneThreads) void lane_tables_kernel(const int32_t* __restrict__ ids, uint32_t n_tok,
+                                                                   uint32_t k, uint32_t n_exp, LaneBases b,
+                                                                   int32_t* __restrict__ tok, int32_t* __restrict__ pair,
+                                                                   int32_t* __restrict__ cnt, int32_t* __restrict__ xrow,
+                                                                   const void** __restrict__ wg,
+                                                                   const void** __restrict__ wu,
+                                                                   const void** __restrict__ wd,
+                                                                   int32_t* __restrict__ order) {
+  __shared__ int count[kMaxExperts], start[kMaxExperts], estart[kMaxExperts];
+  __shared__ int row_of[OSMOS_LANE_MAX_PAIRS];
+  __shared__ int n_entries;
+  const uint32_t n = n_tok * k, e = threadIdx.x;
+  count[e] = 0;
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < n; i += kLaneThreads) atomicAdd(&count[ids[i]], 1);
+  __syncthreads();
+  const int c = e < n_exp ? count[e] : 0, ne = (c + MV_MAX_TOKENS - 1) / MV_MAX_TOKENS;
+  start[e] = c, estart[e] = ne;
+  __syncthreads();
+  for (uint32_t d = 1; d < kMaxExperts; d <<= 1) {  // inclusive scans, then each less its own
+    const int a = e >= d ? start[e - d] : 0, bb = e >= d ? estart[e - d] : 0;
+    __syncthreads();
+    start[e] += a, estart[e] += bb;
+    __syncthreads();
+  }
+  if (e == kMaxExperts - 1) n_entries = estart[e];
+  start[e] -= c, estart[e] -= ne;
+  __syncthreads();
+  // each pick's row: its expert's first plus the expert's picks before it (sorted by expert, then pick)
+  for (uint32_t i = threadIdx.x; i < n; i += kLaneThreads) {
+    const int32_t ex = ids[i];
+    int rank = 0;
+    for (uint32_t j = 0; j < i; j++) rank += ids[j] == ex;
+    const int r = start[ex] + rank;
+    row_of[i] = r, tok[r] = (int32_t) (i / k), pair[r] = (int32_t) i;
+  }
+  // each expert's entries of at most MV_MAX_TOKENS rows, in order
+  if (c)
+    for (int p = 0; p < ne; p++) {
+      const int en = estart[e] + p;
+      cnt[en] = c - p * MV_MAX_TOKENS < MV_MAX_TOKENS ? c - p * MV_MAX_TOKENS : MV_MAX_TOKENS;
+      xrow[en] = start[e] + p * MV_MAX_TOKENS;
+      wg[en] = b.base[0] + (uint64_t) e * b.bytes[0];
+      wu[en] = b.base[1] + (uint64_t) e * b.bytes[1];
+      wd[en] = b.base[2] + (uint64_t) e * b.bytes[2];
+    }
+  __syncthreads();
+  for (uint32_t en = (uint32_t) n_entries + threadIdx.x; en < n; en += kLaneThreads) cnt[en] = 0, xrow[en] = 0;
+  // a token's rows in ascending order (its experts ascending: rows ascend by expert)
+  for (uint32_t t = threadIdx.x; t < n_tok; t += kLaneThreads) {
+    int r[kMaxK];
+    for (uint32_t j = 0; j < k; j++) {
+      int v = row_of[t * k + j], q = (int) j;
+      while (q > 0 && r[q - 1] > v) r[q] = r[q - 1], q--;
+      r[q] = v;
+    }
+    for (uint32_t j = 0; j < k; j++) order[t * k + j] = r[j];
+  }
+}
+
+inline unsigned grid256(uint64_t n) { return (unsigned) ((n + 255) / 256); }
+
+}  // namespace moe
+}  // namespace osm
+
+using namespace osm;
+
+extern "C" OSM_API bool q4x_route(const float* logits, uint32_t n_tok, uint32_t n_exp, uint32_t k, int32_t* ids,
+                                  float* w, int32_t* rows, void* stream) {
+  if (!logits || !ids || !w || !rows || !n_tok || !n_exp || n_exp > moe::kMaxExperts || !k || k > moe::kMaxK ||
+      k > n_exp)
+    return false;
+  moe::route_kernel<<<n_tok, moe::kRouteThreads, 0, (hipStream_t) stream>>>(logits, n_exp, k, ids, w, rows);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API void q4x_expert_bounds(uint32_t n, uint32_t n_exp, Q4xExpertBounds* b) {
+  const uint32_t most = n < n_exp ? n : n_exp;
+  const uint32_t cap[Q4X_TILE_RUNS] = {most, n / 17 < most ? n / 17 : most, n / 33 < most ? n / 33 : most, n / 65};
+  b->entries = 0;
+  for (int r = 0; r < Q4X_TILE_RUNS; r++) b->first[r] = b->entries, b->count[r] = cap[r], b->entries += cap[r];
+  b->slots = n + (moe::kTile - 1) * most;
+}
+
+extern "C" OSM_API bool q4x_expert_tiles(const int32_t* ids, uint32_t n, uint32_t k, uint32_t n_exp, uint32_t dim,
+                                         uint32_t ff, const Q4xExpertTiles* t, void* stream) {
+  if (!ids || !n || !k || n % k || !n_exp || n_exp > moe::kMaxExperts || !dim || !ff || !t || !t->cnt || !t->gidx ||
+      !t->hidx || !t->xg || !t->yg || !t->xd || !t->yd || !t->where || !t->off)
+    return false;
+  for (int j = 0; j < Q4X_GROUP_TENSORS; j++)
+    if ((!t->tab[j] && (!t->base[j] || !t->bytes[j])) || !t->ptr[j]) return false;
+  Q4xExpertBounds bd;
+  q4x_expert_bounds(n, n_exp, &bd);
+  const hipStream_t s = (hipStream_t) stream;
+  moe::tiles_kernel<<<1, moe::kTileThreads, 0, s>>>(ids, n, k, n_exp, dim, ff, *t, bd);
+  if (hipGetLastError() != hipSuccess) return false;
+  if (n > moe::kPlaceInline) moe::place_kernel<<<n_exp, moe::kPlaceThreads, 0, s>>>(ids, n, k, n_exp, *t);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool q4x_moe_sum(const float* y, const int32_t* where, const float* w, uint32_t n_tok, uint32_t k,
+                                    uint32_t dim, const float* shared, const float* shared_logit, float* out,
+                                    void* stream) {
+  if (!y || !where || !w || !shared || !shared_logit || !out || !n_tok || !k || !dim) return false;
+  moe::moe_sum_kernel<<<moe::grid256((uint64_t) n_tok * dim), 256, 0, (hipStream_t) stream>>>(y, where, w, n_tok, k, dim,
+                                                                                             shared, shared_logit, out);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool ops_swiglu_lane(const float* g, const float* u, uint32_t n, float lim, const float* scale,
+                                        uint32_t n_tok, float* h, void* stream) {
+  if (!g || !u || !h || !n || !n_tok || !scale) return false;
+  moe::swiglu_lane_kernel<<<moe::grid256((uint64_t) n * n_tok), 256, 0, (hipStream_t) stream>>>(g, u, n, lim, scale,
+                                                                                               n_tok, h);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool ops_gather_rows(float* dst, const float* src, const int32_t* idx, uint32_t n, uint32_t len,
+                                        void* stream) {
+  if (!dst || !src || !idx || !n || !len) return false;
+  moe::gather_rows_kernel<<<moe::grid256((uint64_t) n * len), 256, 0, (hipStream_t) stream>>>(dst, src, idx, n, len);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool ops_gather_sum_add(float* y, const float* src, const int32_t* idx, uint32_t m, uint32_t n,
+                                           uint32_t dim, const float* add, void* stream) {
+  if (!y || !src || !idx || !m || !n || !dim || !add) return false;
+  moe::gather_sum_kernel<<<moe::grid256((uint64_t) n * dim), 256, 0, (hipStream_t) stream>>>(y, src, idx, m, n, dim, add);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool osmos_lane_tables(const int32_t* ids, uint32_t n_tok, uint32_t k, uint32_t n_exp,
+                                          const void* const* base, const uint64_t* bytes, int32_t* tok, int32_t* pair,
+                                          int32_t* cnt, int32_t* xrow, const void** wg, const void** wu,
+                                          const void** wd, int32_t* order, void* stream) {
+  if (!ids || !n_tok || !k || k > moe::kMaxK || !n_exp || n_exp > moe::kMaxExperts ||
+      (uint64_t) n_tok * k > OSMOS_LANE_MAX_PAIRS || !base || !bytes || !tok || !pair || !cnt || !xrow || !wg || !wu ||
+      !wd || !order)
+    return false;
+  moe::LaneBases b;
+  for (int i = 0; i < 3; i++) b.base[i] = (const uint8_t*) base[i], b.bytes[i] = bytes[i];
+  moe::lane_tables_kernel<<<1, moe::kLaneThreads, 0, (hipStream_t) stream>>>(ids, n_tok, k, n_exp, b, tok, pair, cnt,
+                                                                            xrow, wg, wu, wd, order);
+  return hipGetLastError() == hipSuccess;
+}

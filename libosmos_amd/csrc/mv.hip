@@ -1,0 +1,223 @@
+// libosmos MI355X - the decode's fp32-activation matvec (include/osmos/gpu/mv.h): mv_run, mv_strided, mv_group,
+// mv_group_tok.
+//
+// contract (reference kernels/mv.h:1-70, include/osmos/gpu/mv.h:31-62): a row's 8-value chunks c go to logical lane
+// c % 32 in ascending order, each chunk's 8 values fmaf'd onto the lane's sum in order (the value decode.h gives, the
+// reference's bits), then the 32 lanes' xor tree. any tiling of rows and tokens gives the same bits.
+//
+// CDNA4 mapping: each half of a wave64 is one 32-lane row group holding R rows; a workgroup is 4 waves = 8 R rows.
+// tokens past MV_MAX_TOKENS are tiled 8 at a time over blockIdx.y.
+#include "decode.h"
+
+extern "C" {
+#include "../../include/osmos/gpu/mv.h"
+}
+
+namespace osm {
+namespace mv {
+
+__constant__ DecodeTables kDec = make_decode_tables();
+
+constexpr int kWaves = 4, kThreads = kWave * kWaves, kHalf = 32;
+
+// R rows of one half-wave over NT tokens: x rows xs floats apart (token t's at x + t xs), y's ys apart; rows past
+// `rows` decode row 0 and store nothing; tokens at or past `live` read the last live token and store nothing
+template <uint32_t T, int NT, int R>
+__device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* __restrict__ x,
+                               uint32_t xs, float* __restrict__ y, uint32_t ys, uint32_t live) {
+  const int lane = threadIdx.x % kHalf;
+  const uint32_t row0 = ((blockIdx.x * kWaves + threadIdx.x / kWave) * 2 + (threadIdx.x % kWave) / kHalf) * R;
+  if (row0 >= rows) return;  // the whole half-wave: its tree's partners are its own
+  const uint8_t* base[R];
+#pragma unroll
+  for (int q = 0; q < R; q++) base[q] = w + (uint64_t) (row0 + q < rows ? row0 + q : 0) * row_bytes<T>(cols);
+  const float* xt[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) xt[t] = x + (uint64_t) ((uint32_t) t < live ? t : live - 1) * xs;
+  const uint32_t chunks = cols / kChunk;
+  float acc[R][NT];
+#pragma unroll
+  for (int q = 0; q < R; q++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[q][t] = 0.0f;
+#pragma unroll 2
+  for (uint32_t c = lane; c < chunks; c += kHalf) {
+    float v[R][kChunk];
+#pragma unroll
+    for (int q = 0; q < R; q++) {
+      int k;
+      const uint8_t* b = chunk_at<T>(base[q], c, &k);
+      decode<T>(kDec, b, k, v[q]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const float4 a = ((const float4*) (xt[t] + (uint64_t) c * kChunk))[0];
+      const float4 b = ((const float4*) (xt[t] + (uint64_t) c * kChunk))[1];
+#pragma unroll
+      for (int q = 0; q < R; q++) {
+        float s = acc[q][t];
+        s = __builtin_fmaf(v[q][0], a.x, s), s = __builtin_fmaf(v[q][1], a.y, s);
+        s = __builtin_fmaf(v[q][2], a.z, s), s = __builtin_fmaf(v[q][3], a.w, s);
+        s = __builtin_fmaf(v[q][4], b.x, s), s = __builtin_fmaf(v[q][5], b.y, s);
+        s = __builtin_fmaf(v[q][6], b.z, s), s = __builtin_fmaf(v[q][7], b.w, s);
+        acc[q][t] = s;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < R; q++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      float s = acc[q][t];
+#pragma unroll
+      for (int o = kHalf / 2; o > 0; o >>= 1) s = __fadd_rn(s, __shfl_xor(s, o, kWave));
+      if (lane == 0 && row0 + q < rows && (uint32_t) t < live) y[(uint64_t) t * ys + row0 + q] = s;
+    }
+}
+
+// one matrix, n_tok tokens in tiles of NT over blockIdx.y
+template <uint32_t T, int NT, int R>
+__global__ __launch_bounds__(kThreads) void kernel(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols,
+                                                   const float* __restrict__ x, uint32_t xs, uint32_t n_tok,
+                                                   float* __restrict__ y, uint32_t ys) {
+  const uint32_t t0 = blockIdx.y * NT, live = n_tok - t0 < (uint32_t) NT ? n_tok - t0 : NT;
+  rows_of<T, NT, R>(w, rows, cols, x + (uint64_t) t0 * xs, xs, y + (uint64_t) t0 * ys, ys, live);
+}
+
+// n matrices of one shape (blockIdx.y the matrix): x at x + (m / x_div) x_mat, y at y + m rows
+template <uint32_t T, int R>
+__global__ __launch_bounds__(kThreads) void group_kernel(const uint8_t* const* __restrict__ w, uint32_t rows,
+                                                         uint32_t cols, const float* __restrict__ x, uint32_t x_mat,
+                                                         uint32_t x_div, float* __restrict__ y) {
+  const uint32_t m = blockIdx.y;
+  rows_of<T, 1, R>(w[m], rows, cols, x + (uint64_t) (m / x_div) * x_mat, cols, y + (uint64_t) m * rows, rows, 1);
+}
+
+// matrices each over their own cnt[m] tokens from row xrow[m] (0: skipped)
+template <uint32_t T, int NT, int R>
+__global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* const* __restrict__ w,
+                                                             const int32_t* __restrict__ cnt,
+                                                             const int32_t* __restrict__ xrow, uint32_t rows,
+                                                             uint32_t cols, const float* __restrict__ x, uint32_t xs,
+                                                             float* __restrict__ y, uint32_t ys) {
+  const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
+  if (!n) return;
+  const uint64_t r0 = (uint64_t) xrow[m];
+  rows_of<T, NT, R>(w[m], rows, cols, x + r0 * xs, xs, y + r0 * ys, ys, n < (uint32_t) NT ? n : NT);
+}
+
+constexpr int kR = 2;  // rows a half-wave: the tiling alone, never the bits
+
+template <uint32_t T, int NT>
+bool run_nt(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t xs, uint32_t n_tok, float* y,
+            uint32_t ys, hipStream_t s) {
+  constexpr uint32_t per = kWaves * 2 * kR;
+  const dim3 grid((rows + per - 1) / per, (n_tok + NT - 1) / NT);
+  kernel<T, NT, kR><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <uint32_t T>
+bool by_tokens(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t xs, uint32_t n_tok, float* y,
+               uint32_t ys, hipStream_t s) {
+  if (!w || !x || !y || !rows || !cols || cols % Block<T>::values || cols % kChunk || !n_tok) return false;
+  if ((n_tok > 1 && (xs < cols || ys < rows)) || xs % kChunk) return false;
+  switch (n_tok) {
+    case 1: return run_nt<T, 1>(w, rows, cols, x, xs, n_tok, y, ys, s);
+    case 2: return run_nt<T, 2>(w, rows, cols, x, xs, n_tok, y, ys, s);
+    case 3: return run_nt<T, 3>(w, rows, cols, x, xs, n_tok, y, ys, s);
+    case 4: return run_nt<T, 4>(w, rows, cols, x, xs, n_tok, y, ys, s);
+    default: return run_nt<T, 8>(w, rows, cols, x, xs, n_tok, y, ys, s);  // 5 .. any: tiles of 8
+  }
+}
+
+template <uint32_t T>
+bool group(const void* const* w, uint32_t n, uint32_t rows, uint32_t cols, const float* x, uint32_t x_mat,
+           uint32_t x_div, float* y, hipStream_t s) {
+  if (!w || !x || !y || cols % Block<T>::values || cols % kChunk || x_mat % kChunk || !x_div) return false;
+  constexpr uint32_t per = kWaves * 2 * kR;
+  group_kernel<T, kR><<<dim3((rows + per - 1) / per, n), kThreads, 0, s>>>((const uint8_t* const*) w, rows, cols, x,
+                                                                            x_mat, x_div, y);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <uint32_t T, int NT>
+bool group_tok_nt(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n, uint32_t rows,
+                  uint32_t cols, const float* x, uint32_t xs, float* y, uint32_t ys, hipStream_t s) {
+  constexpr uint32_t per = kWaves * 2 * kR;
+  group_tok_kernel<T, NT, kR><<<dim3((rows + per - 1) / per, n), kThreads, 0, s>>>(
+      (const uint8_t* const*) w, cnt, xrow, rows, cols, x, xs, y, ys);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <uint32_t T>
+bool group_tok(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n, uint32_t max_cnt,
+               uint32_t rows, uint32_t cols, const float* x, uint32_t xs, float* y, uint32_t ys, hipStream_t s) {
+  if (!w || !cnt || !xrow || !x || !y || cols % Block<T>::values || cols % kChunk || xs < cols || xs % kChunk)
+    return false;
+  switch (max_cnt) {
+    case 1: return group_tok_nt<T, 1>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 2: return group_tok_nt<T, 2>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 3: return group_tok_nt<T, 3>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 4: return group_tok_nt<T, 4>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 5: return group_tok_nt<T, 5>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 6: return group_tok_nt<T, 6>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 7: return group_tok_nt<T, 7>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    case 8: return group_tok_nt<T, 8>(w, cnt, xrow, n, rows, cols, x, xs, y, ys, s);
+    default: return false;
+  }
+}
+
+#define OSM_MV_TYPES(X) \
+  X(kF32) X(kBF16) X(kQ8_0) X(kQ4_0) X(kIQ4_NL) X(kQ2_K) X(kQ3_K) X(kQ4_K) X(kQ5_K) X(kQ6_K) X(kIQ2_XXS) X(kIQ2_XS) \
+  X(kIQ2_S) X(kIQ3_XXS) X(kIQ1_S) X(kIQ1_M) X(kIQ4_XS)
+
+}  // namespace mv
+}  // namespace osm
+
+using namespace osm;
+
+extern "C" OSM_API bool mv_strided(uint32_t type, const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t xs,
+                           uint32_t n_tok, float* y, uint32_t ys, void* stream) {
+  const hipStream_t s = (hipStream_t) stream;
+  switch (type) {
+#define X(t) \
+  case t: return mv::by_tokens<t>(w, rows, cols, x, xs, n_tok, y, ys, s);
+    OSM_MV_TYPES(X)
+#undef X
+    default: return false;
+  }
+}
+
+extern "C" OSM_API bool mv_run(uint32_t type, const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t n_tok,
+                       float* y, void* stream) {
+  if (n_tok > MV_MAX_TOKENS) return false;
+  return mv_strided(type, w, rows, cols, x, cols, n_tok, y, rows, stream);
+}
+
+extern "C" OSM_API bool mv_group(uint32_t type, const void* const* w, uint32_t n, uint32_t rows, uint32_t cols, const float* x,
+                         uint32_t x_mat, uint32_t x_div, float* y, void* stream) {
+  if (!n || n > MV_MAX_GROUP || !rows) return false;
+  const hipStream_t s = (hipStream_t) stream;
+  switch (type) {
+#define X(t) \
+  case t: return mv::group<t>(w, n, rows, cols, x, x_mat, x_div, y, s);
+    OSM_MV_TYPES(X)
+#undef X
+    default: return false;
+  }
+}
+
+extern "C" OSM_API bool mv_group_tok(uint32_t type, const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n,
+                             uint32_t max_cnt, uint32_t rows, uint32_t cols, const float* x, uint32_t xs, float* y,
+                             uint32_t ys, void* stream) {
+  if (!n || n > MV_MAX_GROUP || !rows || !max_cnt || max_cnt > MV_MAX_TOKENS) return false;
+  const hipStream_t s = (hipStream_t) stream;
+  switch (type) {
+#define X(t) \
+  case t: return mv::group_tok<t>(w, cnt, xrow, n, max_cnt, rows, cols, x, xs, y, ys, s);
+    OSM_MV_TYPES(X)
+#undef X
+    default: return false;
+  }
+}

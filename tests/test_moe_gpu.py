@@ -1,0 +1,224 @@
+"""The MoE plumbing and the whole routed lane layer on the MI355X through the C ABI: q4x_route, q4x_expert_tiles,
+q4x_moe_sum, ops_* and osmos_lane_tables against independent restatements of their documented contracts, and
+osmos_lane_layer bit for bit against the reference CPU lane's golden layer and the oracle at batches 1 / 4 / 32.
+(reference: include/osmos/gpu/q4x_ops.h:356-384, tests/gpu/test_q4x_moe_gpu.hip, tests/test_cpu_lane.c)"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+
+from libosmos_amd import capi, synth
+from oracle import orc
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def g():
+    import torch  # noqa: F401
+    from tests import gpu_util
+    return gpu_util
+
+
+def test_route(g):
+    """ids: the k greatest softmax probabilities (lowest id among equals) - exact; weights p / sum within 1e-6 (the
+    device's exp and the host's need not agree to the bit); rows[t k + j] = t"""
+    import torch
+    rng = np.random.default_rng(1)
+    for n_exp, k, n_tok in [(512, 10, 7), (256, 8, 33), (64, 4, 3), (1024, 32, 2)]:
+        logits = rng.normal(0, 2, (n_tok, n_exp)).astype(np.float32)
+        logits[0, 5] = logits[0, 9] = logits[0].max() + 1  # a tie: the lower id first
+        ids = torch.zeros(n_tok * k, dtype=torch.int32, device="cuda")
+        w = torch.zeros(n_tok * k, dtype=torch.float32, device="cuda")
+        rows = torch.zeros(n_tok * k, dtype=torch.int32, device="cuda")
+        g.call("q4x_route", g.a(g.dev(logits)), n_tok, n_exp, k, g.a(ids), g.a(w), g.a(rows), None)
+        oi = np.zeros(n_tok * k, np.int32)
+        ow = np.zeros(n_tok * k, np.float32)
+        orc.orc().orc_route(orc.ptr(logits), n_tok, n_exp, k, orc.ptr(oi), orc.ptr(ow))
+        assert (g.host(ids) == oi).all()
+        assert ids[0].item() == 5 and ids[1].item() == 9
+        assert np.allclose(g.host(w), ow, rtol=1e-6, atol=0)
+        assert (g.host(rows) == np.repeat(np.arange(n_tok), k)).all()
+
+
+def tiles_ref(ids, k, n_exp, dim, ff, bases, nbytes):
+    """q4x_expert_tiles' contract restated on the host (a stable sort by expert)"""
+    n = len(ids)
+    bd = capi.Q4xExpertBounds()
+    capi.lib().q4x_expert_bounds(n, n_exp, ctypes.byref(bd))
+    order = np.argsort(ids, kind="stable")
+    where = np.empty(n, np.int64)
+    where[order] = np.arange(n)
+    count = np.bincount(ids, minlength=n_exp)
+    place0 = np.concatenate([[0], np.cumsum(count)[:-1]])
+    tiles = (count + 15) // 16 * 16
+    slot0 = np.concatenate([[0], np.cumsum(tiles)[:-1]])
+    gidx = -np.ones(bd.slots, np.int64)
+    hidx = -np.ones(bd.slots, np.int64)
+    for i in range(n):
+        e = ids[i]
+        q = where[i]
+        gidx[slot0[e] + q - place0[e]] = i // k
+        hidx[slot0[e] + q - place0[e]] = q
+    entries = {r: [] for r in range(4)}
+    for e in range(n_exp):
+        c = int(count[e])
+        for part in range((c + 127) // 128):
+            m = min(128, c - part * 128)
+            r = 0 if m <= 16 else 1 if m <= 32 else 2 if m <= 64 else 3
+            slot, place = slot0[e] + part * 128, place0[e] + part * 128
+            entries[r].append((m, slot * dim, slot * ff, place * ff, place * dim,
+                               [bases[j] + e * nbytes[j] for j in range(3)]))
+    return bd, where, gidx, hidx, entries
+
+
+def test_expert_tiles(g):
+    import torch
+    rng = np.random.default_rng(2)
+    for n_tok, k, n_exp in [(3, 10, 512), (512, 8, 256), (40, 4, 64)]:
+        if n_tok == 512:  # Zipf(1.1) load skew, distinct experts a token
+            p = 1.0 / np.arange(1, n_exp + 1) ** 1.1
+            p /= p.sum()
+            ids = np.concatenate([rng.choice(n_exp, k, replace=False, p=p) for _ in range(n_tok)]).astype(np.int32)
+        else:
+            ids = np.concatenate([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+        n = len(ids)
+        dim, ff = 2048, 512
+        bases, nbytes = [0x10000000, 0x20000000, 0x30000000], [4096, 4096, 8192]
+        bd, where, gidx, hidx, entries = tiles_ref(ids, k, n_exp, dim, ff, bases, nbytes)
+        E, S = bd.entries, bd.slots
+        T = lambda m, dt=torch.int32: torch.full((m,), -7, dtype=dt, device="cuda")  # noqa: E731
+        cnt, gi, hi, wh, off = T(E), T(S), T(S), T(n), T(3 * n_exp)
+        xg, yg, xd, yd = (T(E, torch.int32) for _ in range(4))
+        ptrs = [torch.zeros(E, dtype=torch.int64, device="cuda") for _ in range(3)]
+        t = capi.Q4xExpertTiles()
+        for j in range(3):
+            t.base[j], t.bytes[j], t.tab[j], t.ptr[j] = bases[j], nbytes[j], None, ptrs[j].data_ptr()
+        t.cnt, t.gidx, t.hidx, t.where, t.off = cnt.data_ptr(), gi.data_ptr(), hi.data_ptr(), wh.data_ptr(), off.data_ptr()
+        t.xg, t.yg, t.xd, t.yd = xg.data_ptr(), yg.data_ptr(), xd.data_ptr(), yd.data_ptr()
+        g.call("q4x_expert_tiles", g.a(g.dev(ids)), n, k, n_exp, dim, ff, ctypes.byref(t), None)
+        assert (g.host(wh) == where).all()
+        assert (g.host(gi) == gidx).all() and (g.host(hi) == hidx).all()
+        ch = g.host(cnt)
+        host = {nm: g.host(v).astype(np.int64) for nm, v in [("xg", xg), ("xd", xd), ("yg", yg), ("yd", yd)]}
+        ph = [g.host(p_) for p_ in ptrs]
+        for r in range(4):
+            live = entries[r]
+            for i in range(bd.count[r]):
+                en = bd.first[r] + i
+                if i < len(live):
+                    m, a, b, c, d, pp = live[i]
+                    assert ch[en] == m and host["xg"][en] == a and host["xd"][en] == b
+                    assert host["yg"][en] == c and host["yd"][en] == d
+                    assert [ph[j][en] for j in range(3)] == pp
+                else:
+                    assert ch[en] == 0
+
+
+def test_moe_sum_and_ops(g):
+    import torch
+    rng = np.random.default_rng(3)
+    n_tok, k, dim = 5, 4, 256
+    y = rng.normal(0, 1, (n_tok * k, dim)).astype(np.float32)
+    where = rng.permutation(n_tok * k).astype(np.int32)
+    w = rng.uniform(0, 1, n_tok * k).astype(np.float32)
+    sh = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    sl = rng.normal(0, 1, n_tok).astype(np.float32)
+    out = torch.zeros((n_tok, dim), device="cuda")
+    g.call("q4x_moe_sum", g.a(g.dev(y)), g.a(g.dev(where)), g.a(g.dev(w)), n_tok, k, dim, g.a(g.dev(sh)), g.a(g.dev(sl)),
+           g.a(out), None)
+    want = np.zeros((n_tok, dim), np.float32)
+    orc.orc().orc_moe_sum(orc.ptr(y), orc.ptr(where), orc.ptr(w), n_tok, k, dim, orc.ptr(sh), orc.ptr(sl), orc.ptr(want))
+    assert np.allclose(g.host(out), want, rtol=1e-6, atol=1e-6)
+    # the weighted sum before the gate is exact to the order: compare with the gate's term removed
+    out0 = torch.zeros((n_tok, dim), device="cuda")
+    g.call("q4x_moe_sum", g.a(g.dev(y)), g.a(g.dev(where)), g.a(g.dev(w)), n_tok, k, dim,
+           g.a(g.dev(np.zeros_like(sh))), g.a(g.dev(sl)), g.a(out0), None)
+    want0 = np.zeros((n_tok, dim), np.float32)
+    for j in range(k):
+        want0 = (want0 + (y[where.reshape(n_tok, k)[:, j]] * w.reshape(n_tok, k)[:, j:j + 1]).astype(np.float32))
+    assert (g.bits(g.host(out0)) == g.bits(want0 + np.float32(0))).all()
+    # gather_sum_add: the sum in j's order, then add's
+    idx = rng.integers(0, n_tok * k, n_tok * k).astype(np.int32)
+    add = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    o = torch.zeros((n_tok, dim), device="cuda")
+    g.call("ops_gather_sum_add", g.a(o), g.a(g.dev(y)), g.a(g.dev(idx)), k, n_tok, dim, g.a(g.dev(add)), None)
+    want = np.zeros((n_tok, dim), np.float32)
+    orc.orc().orc_gather_sum_add(orc.ptr(want), orc.ptr(y), orc.ptr(idx), k, n_tok, dim, orc.ptr(add))
+    assert (g.bits(g.host(o)) == g.bits(want)).all()
+    # swiglu_lane: lane_swiglu's bits
+    gg, uu = rng.normal(0, 3, (3, 64)).astype(np.float32), rng.normal(0, 3, (3, 64)).astype(np.float32)
+    sc = rng.uniform(0, 1, 3).astype(np.float32)
+    h = torch.zeros((3, 64), device="cuda")
+    g.call("ops_swiglu_lane", g.a(g.dev(gg)), g.a(g.dev(uu)), 64, 2.5, g.a(g.dev(sc)), 3, g.a(h), None)
+    L = orc.orc()
+    want = np.array([[L.orc_lane_swiglu(float(a), float(b), 2.5, float(sc[t])) for a, b in zip(gg[t], uu[t])]
+                     for t in range(3)], np.float32)
+    assert (g.bits(g.host(h)) == g.bits(want)).all()
+
+
+def _lane_layer_oracle(type_, x, ids, wts, gate, up, down, dim, ff, lim):
+    """the reference CPU lane's layer (oracle): pairs sorted by (expert, pick), tokens' rows in ascending expert id"""
+    n_tok, k = ids.shape
+    pairs = sorted((int(ids[t, j]), t * k + j) for t in range(n_tok) for j in range(k))
+    rows_x = np.stack([x[m // k] for _, m in pairs]).astype(np.float32)
+    scale = np.array([wts.reshape(-1)[m] for _, m in pairs], np.float32)
+    experts = sorted(set(e for e, _ in pairs))
+    row0 = np.array([min(r for r, (e, _) in enumerate(pairs) if e == ex) for ex in experts], np.uint32)
+    cnt = np.array([sum(1 for e, _ in pairs if e == ex) for ex in experts], np.uint32)
+    P = ctypes.c_void_p
+    tab = lambda mats: (P * len(experts))(*[mats[e].ctypes.data for e in experts])  # noqa: E731
+    ye = np.zeros((len(pairs), dim), np.float32)
+    assert orc.orc().orc_lane_layer(type_, type_, dim, ff, lim, orc.ptr(rows_x), orc.ptr(scale), len(pairs), tab(gate),
+                                    tab(up), tab(down), orc.ptr(row0), orc.ptr(cnt), len(experts), orc.ptr(ye))
+    row_of = {m: r for r, (_, m) in enumerate(pairs)}
+    order = np.array([sorted(row_of[t * k + j] for j in range(k)) for t in range(n_tok)], np.int32).reshape(-1)
+    out = np.zeros((n_tok, dim), np.float32)
+    orc.orc().orc_gather_sum_add(orc.ptr(out), orc.ptr(ye), orc.ptr(order), k, n_tok, dim, None)
+    return out
+
+
+def test_lane_layer_golden(g):
+    """osmos_lane_layer on the golden layer (the reference CPU lane's bits): dim 512, ff 256, IQ3_XXS, top-2 of 4"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    gd = np.load(os.path.join(GOLD, "golden_layer.npz"))
+    t3 = synth.ID["IQ3_XXS"]
+    gate, up, down = (g.dev(np.ascontiguousarray(gd[k_])) for k_ in ("gate", "up", "down"))
+    L = LaneLayer(t3, t3, 512, 256, 4, 2, gate.reshape(4, -1), up.reshape(4, -1), down.reshape(4, -1))
+    out = torch.full((3, 512), float("nan"), device="cuda")
+    L.forward(g.dev(gd["x"]), g.dev(gd["ids"].astype(np.int32)), g.dev(gd["wts"]), torch.zeros((3, 512), device="cuda"),
+              out)
+    assert (g.bits(g.host(out)) == g.bits(gd["out"])).all()
+
+
+@pytest.mark.parametrize("n_tok", [1, 4, 32])
+def test_lane_layer_qwen_shape(g, n_tok):
+    """the config's MoE layer shape (hidden 2048, expert ff 512, top-10) over 64 experts: the oracle's bits at each
+    batch, and each token's bits its own (the batch of 1 row by row)"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t3 = synth.ID["IQ3_XXS"]
+    n_exp, k, dim, ff = 64, 10, 2048, 512
+    rng = np.random.default_rng(n_tok)
+    gate = [synth.iq_blocks(t3, ff, dim, 1000 + e) for e in range(n_exp)]
+    up = [synth.iq_blocks(t3, ff, dim, 2000 + e) for e in range(n_exp)]
+    down = [synth.iq_blocks(t3, dim, ff, 3000 + e) for e in range(n_exp)]
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    wts = rng.uniform(0.01, 0.3, (n_tok, k)).astype(np.float32)
+    want = _lane_layer_oracle(t3, x, ids, wts, gate, up, down, dim, ff, math.inf)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(t3, t3, dim, ff, n_exp, k, D(gate), D(up), D(down))
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("lane layer", n_tok, flush=True)
+    L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
+    if n_tok > 1:
+        one = torch.full((1, dim), float("nan"), device="cuda")
+        for t in (0, n_tok - 1):
+            L.forward(g.dev(x[t:t + 1]), g.dev(ids[t:t + 1]), g.dev(wts[t:t + 1]), torch.zeros((1, dim), device="cuda"), one)
+            assert (g.bits(g.host(one)[0]) == g.bits(want[t])).all()
