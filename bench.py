@@ -1,0 +1,276 @@
+"""bench.py - libosmos MI355X's headline benchmark on one MI355X.
+
+Headline (value): the Qwen-style 512-expert MoE layer in IQ3_XXS at batch 1 (hidden 2048, expert
+ff 512, top-10 of 512) - one step is one routed layer through the C ABI's osmos_lane_layer (round x, device-built
+tables, fused gate/up + SwiGLU, round h, down, ascending-expert token sums), bit-exact to the reference CPU lane.
+value = algorithmic bytes a step (each distinct routed expert's gate + up + down once, x in, the output out) / time a
+step, in GB/s; weights resident in HBM and rotated through more than 2 GiB of layer copies so the 256 MB Infinity Cache
+cannot serve them; steps captured in a HIP graph (the decode's launch pattern), timed with events between
+synchronizations.
+
+roofline: the dominant kernel (the fused gate/up launch of that layer) timed alone, its algorithmic bytes a launch over
+its average duration (events on the launching stream), against MI355X's 8 TB/s.
+cpu_baseline: the reference's own CPU path (oracle/_ref: src/cpu/q8.c's cpu_q8_rows and kernels/lane.h) on the host's
+cores for the same layer, rows split evenly over the threads as src/cpu/lane.c splits them.
+
+--all adds the other BASELINE configs as `extra` lines (Q4_0 / Q4_K / Q3_K GEMV, the DeepSeek IQ1 experts, the mmq
+expert GEMM) - they are reported, not the headline.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "quant GEMV GB/s (% HBM peak) bs=1; expert GEMM int8 TOPS (% MFMA) bs=512"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Events:
+    """elapsed ms between two points on the current stream"""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, reps):
+        t = self.torch
+        s = t.cuda.current_stream()
+        a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        t.cuda.synchronize()
+        a.record(s)
+        for _ in range(reps):
+            fn()
+        b.record(s)
+        t.cuda.synchronize()
+        return a.elapsed_time(b)
+
+
+def iq_weights(torch, gen, n_blocks, block_bytes, d_at=0, sigma=0.02):
+    """IQ blocks on the device: uniform random bytes (grid indices, signs, sub-scales), each block's f16 scale
+    |N(0, sigma)| at byte d_at (the BASELINE configs' weights)"""
+    raw = torch.randint(0, 256, (n_blocks, block_bytes), dtype=torch.uint8, device="cuda", generator=gen)
+    d = (torch.randn(n_blocks, device="cuda", generator=gen).abs_() * sigma).half().view(torch.int16).to(torch.int32)
+    raw[:, d_at] = (d & 0xFF).to(torch.uint8)
+    raw[:, d_at + 1] = ((d >> 8) & 0xFF).to(torch.uint8)
+    return raw.reshape(-1)
+
+
+def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=0):
+    """config 3: returns a dict of the step's timing and bytes"""
+    from libosmos_amd.layer import LaneLayer
+    T = 18  # IQ3_XXS
+    dim, ff, n_exp, k = 2048, 512, 512, 10
+    per_expert = 3 * (ff * (dim // 256) * 98)  # gate + up + down: 1,204,224 B
+    n_layers = max(2, math.ceil(rotate_bytes / (per_expert * n_exp)))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        mats = [iq_weights(torch, gen, n_exp * ff * dim // 256, 98).reshape(n_exp, -1) for _ in range(2)]
+        mats.append(iq_weights(torch, gen, n_exp * dim * ff // 256, 98).reshape(n_exp, -1))
+        layers.append(LaneLayer(T, T, dim, ff, n_exp, k, *mats))
+    G = 64  # steps a graph
+    rng = torch.Generator(device="cpu")
+    rng.manual_seed(seed + 1)
+    ids = torch.stack([torch.stack([torch.randperm(n_exp, generator=rng)[:k] for _ in range(n_tok)]) for _ in range(G)])
+    ids = ids.to(torch.int32).cuda()
+    w = torch.softmax(torch.randn(G, n_tok, k, generator=rng), dim=-1).cuda()
+    x = torch.randn(G, n_tok, dim, generator=rng).cuda()
+    add = torch.zeros(n_tok, dim, device="cuda")
+    out = torch.zeros(G, n_tok, dim, device="cuda")
+    for L in layers:
+        L.workspace(n_tok)
+    # algorithmic bytes a step: each distinct expert's three matrices once, x read, the output written
+    distinct = [len(set(ids[s].reshape(-1).tolist())) for s in range(G)]
+    step_bytes = sum(distinct) / G * per_expert + n_tok * dim * 4 * 2 + n_tok * k * 8
+
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for st in range(G):  # one eager pass (also the warm-up of every code path)
+            layers[st % n_layers].forward(x[st], ids[st], w[st], add, out[st], stream=s.cuda_stream)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for st in range(G):
+                layers[st % n_layers].forward(x[st], ids[st], w[st], add, out[st], stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    reps = max(1, steps // G)
+    ev = Events(torch)
+    for _ in range(max(1, warmup // G)):
+        graph.replay()
+    ms = ev.time(graph.replay, reps)
+    n_steps = reps * G
+    ms_step = ms / n_steps
+    return dict(n_tok=n_tok, steps=n_steps, ms_per_step=ms_step, step_bytes=step_bytes,
+                gbs=step_bytes / (ms_step * 1e-3) / 1e9, layers=layers, ids=ids, w=w, x=x, G=G, n_layers=n_layers,
+                dims=(dim, ff, n_exp, k), per_expert=per_expert)
+
+
+def gate_up_kernel_bench(torch, capi, lay, reps=20):
+    """the dominant kernel alone: q8_gate_up over the layer's step tables (built beforehand), back to back in a graph;
+    average duration a launch from events on its stream"""
+    dim, ff, n_exp, k = lay["dims"]
+    layers, ids, G, n_layers = lay["layers"], lay["ids"], lay["G"], lay["n_layers"]
+    n_tok = lay["n_tok"]
+    n = n_tok * k
+    L = capi.lib()
+    i32 = lambda m: torch.zeros(m, dtype=torch.int32, device="cuda")  # noqa: E731
+    tabs = []
+    xq = torch.zeros(n_tok, dim, dtype=torch.int8, device="cuda")
+    xd = torch.zeros(n_tok, dim // 32, device="cuda")
+    L.q8_round(capi.addr(lay["x"][0]), n_tok, dim, dim, capi.addr(xq), capi.addr(xd), None)
+    for st in range(G):
+        lyr = layers[st % n_layers]
+        tb = dict(tok=i32(n), pair=i32(n), cnt=i32(n), xrow=i32(n), order=i32(n),
+                  wg=torch.zeros(n, dtype=torch.int64, device="cuda"), wu=torch.zeros(n, dtype=torch.int64, device="cuda"),
+                  wd=torch.zeros(n, dtype=torch.int64, device="cuda"))
+        base = (ctypes.c_void_p * 3)(lyr.desc.gate, lyr.desc.up, lyr.desc.down)
+        nbytes = (ctypes.c_uint64 * 3)(lyr.desc.gate_bytes, lyr.desc.up_bytes, lyr.desc.down_bytes)
+        assert L.osmos_lane_tables(capi.addr(ids[st]), n_tok, k, n_exp, base, nbytes, *(capi.addr(tb[x]) for x in (
+            "tok", "pair", "cnt", "xrow", "wg", "wu", "wd", "order")), None)
+        tabs.append(tb)
+    h = torch.zeros(n, ff, device="cuda")
+    torch.cuda.synchronize()
+    max_cnt = min(n_tok, 8)
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+
+    def launch_all():
+        for st in range(G):
+            tb = tabs[st]
+            assert L.q8_gate_up(18, capi.addr(tb["wg"]), capi.addr(tb["wu"]), capi.addr(tb["cnt"]), capi.addr(tb["xrow"]),
+                                capi.addr(tb["tok"]), capi.addr(tb["pair"]), n, max_cnt, ff, dim, capi.addr(xq),
+                                capi.addr(xd), capi.addr(lay["w"][st]), math.inf, capi.addr(h), ff, s.cuda_stream)
+
+    with torch.cuda.stream(s):
+        launch_all()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            launch_all()
+    torch.cuda.synchronize()
+    graph.replay()
+    ev = Events(torch)
+    with torch.cuda.stream(s):
+        ms = ev.time(graph.replay, reps)
+    launches = reps * G
+    us = ms * 1e3 / launches
+    distinct = [len(set(ids[st].reshape(-1).tolist())) for st in range(G)]
+    per_launch = sum(distinct) / G * (2 * ff * (dim // 256) * 98) + n_tok * (dim + dim // 32 * 4) + n * ff * 4
+    return dict(us=us, bytes=per_launch, gbs=per_launch / (us * 1e-6) / 1e9)
+
+
+def cpu_baseline(lay, seconds=10.0):
+    """the reference's CPU path on this host's cores for one step of the same layer (bs as the GPU's), a bounded
+    sample: repetitions of the layer until ~`seconds` of CPU time"""
+    import numpy as np
+    from oracle import orc
+    torch = __import__("torch")
+    dim, ff, n_exp, k = lay["dims"]
+    n_tok = lay["n_tok"]
+    R = orc.ref()
+    kind = "reference"
+    if R is None or not R.ref_q8_ready():
+        kind = "port"
+    ids = lay["ids"][0].cpu().numpy()
+    lyr = lay["layers"][0]
+    experts = sorted(set(ids.reshape(-1).tolist()))
+    mats = {}
+    for nm, t in zip(("g", "u", "d"), lyr.tensors):
+        mats[nm] = [t[e].cpu().numpy() for e in experts]
+    pairs = sorted((int(ids[t, j]), t * k + j) for t in range(n_tok) for j in range(k))
+    r0 = np.array([min(r for r, (e, _) in enumerate(pairs) if e == ex) for ex in experts], np.uint32)
+    cnt = np.array([sum(1 for e, _ in pairs if e == ex) for ex in experts], np.uint32)
+    x = lay["x"][0].cpu().numpy()
+    rows_x = np.stack([x[m // k] for _, m in pairs]).astype(np.float32)
+    scale = lay["w"][0].cpu().numpy().reshape(-1)[[m for _, m in pairs]].astype(np.float32)
+    P = ctypes.c_void_p
+    tab = lambda ms: (P * len(experts))(*[m.ctypes.data for m in ms])  # noqa: E731
+    threads = len(os.sched_getaffinity(0))
+    y = np.zeros((len(pairs), dim), np.float32)
+    if kind == "reference":
+        q, d = orc.q8_round(rows_x, R)
+        args = (18, dim, ff, tab(mats["g"]), tab(mats["u"]), tab(mats["d"]), orc.ptr(r0), orc.ptr(cnt), len(experts),
+                len(pairs), orc.ptr(q), orc.ptr(d), orc.ptr(scale), orc.ptr(y), threads)
+        assert R.ref_lane_layer_mt(*args, 3)  # warm-up
+        t0 = time.perf_counter()
+        assert R.ref_lane_layer_mt(*args, 10)
+        per = (time.perf_counter() - t0) / 10
+        reps = max(10, int(seconds / max(per, 1e-6)))
+        t0 = time.perf_counter()
+        assert R.ref_lane_layer_mt(*args, reps)
+        per = (time.perf_counter() - t0) / reps
+    else:
+        threads = 1
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < seconds:
+            assert orc.orc().orc_lane_layer(18, 18, dim, ff, math.inf, orc.ptr(rows_x), orc.ptr(scale), len(pairs),
+                                            tab(mats["g"]), tab(mats["u"]), tab(mats["d"]), orc.ptr(r0), orc.ptr(cnt),
+                                            len(experts), orc.ptr(y))
+            reps += 1
+        per = (time.perf_counter() - t0) / reps
+    del torch
+    step_bytes = len(experts) * lay["per_expert"] + n_tok * dim * 8
+    return {"value": round(step_bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": "%d x one %d-token step of the same layer (%d experts' gate/up/down, int8 lane), %.2f ms a step"
+                      % (reps, n_tok, len(experts), per * 1e3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1280)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--all", action="store_true", help="also the other BASELINE configs, as extra lines")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (--gpus %d refused)" % args.gpus)
+        sys.exit(2)
+    import torch
+    from libosmos_amd import capi
+    capi.lib()
+    torch.cuda.set_device(0)
+    log("config 3 layer, batch 1")
+    lay = moe_layer_bench(torch, capi, 1, args.steps, args.warmup)
+    log("  %.2f us a step, %.1f GB/s" % (lay["ms_per_step"] * 1e3, lay["gbs"]))
+    ker = gate_up_kernel_bench(torch, capi, lay)
+    log("  gate_up kernel: %.2f us, %.1f GB/s" % (ker["us"], ker["gbs"]))
+    line = {
+        "metric": METRIC, "value": round(lay["gbs"], 2), "unit": "GB/s", "n_gpus": 1, "steps": lay["steps"],
+        "warmup": args.warmup, "ms_per_step": round(lay["ms_per_step"], 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "qwen_moe_layer_iq3xxs_bs1", "hidden": 2048, "experts": 512, "expert_ff": 512,
+                   "top_k": 10, "batch": 1, "weights": "IQ3_XXS", "contract": "lane int8 (bit-exact)",
+                   "pct_hbm_peak": round(100 * lay["gbs"] / HBM_PEAK_GBS, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(ker["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ker["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "osm::lane::gate_up_kernel<IQ3_XXS,1,16>", "us_per_launch": round(ker["us"], 3),
+                     "bytes_per_launch": int(ker["bytes"])},
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(lay, args.cpu_seconds)
+    if args.all:
+        extra = {}
+        for n_tok in (4, 32):
+            lb = moe_layer_bench(torch, capi, n_tok, max(args.steps // 4, 64), 64)
+            extra["qwen_moe_layer_iq3xxs_bs%d" % n_tok] = {"GB/s": round(lb["gbs"], 2),
+                                                           "us_per_step": round(lb["ms_per_step"] * 1e3, 3)}
+        line["extra"] = extra
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

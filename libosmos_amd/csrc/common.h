@@ -49,7 +49,7 @@ template <uint32_t T> constexpr uint64_t row_bytes(uint32_t cols) {
 }
 
 // ---- the codebooks: expanded from the packed index lists at compile time, one constant-memory table a grid ----
-struct Grids {
+struct alignas(16) Grids {
   uint64_t iq2xxs[256];
   uint64_t iq2xs[512];
   uint64_t iq2s[1024];
@@ -94,6 +94,19 @@ __device__ inline float f16(uint32_t bits) { return __half2float(__ushort_as_hal
 
 // a 7-bit sign index as 8 signs, bit 7 its parity (gguf's ksigns table, computed)
 __device__ inline uint32_t ksign(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
+
+// ---- cross-lane: the value of lane (this lane ^ o), o in 1 .. 16, within the lane's aligned group of 32 (DPP
+// quad permutes for 1 and 2, ds_swizzle's xor mode for 4 .. 16): the exact xor partner a tree needs ----
+__device__ inline int xor_lane(int x, int o) {
+  if (o == 1) return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+  if (o == 2) return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  switch (o) {  // bitmask mode: source lane = (lane & 31) ^ o
+    case 4: return __builtin_amdgcn_ds_swizzle(x, (4 << 10) | 0x1F);
+    case 8: return __builtin_amdgcn_ds_swizzle(x, (8 << 10) | 0x1F);
+    default: return __builtin_amdgcn_ds_swizzle(x, (16 << 10) | 0x1F);
+  }
+}
+__device__ inline float xor_lane(float v, int o) { return __int_as_float(xor_lane(__float_as_int(v), o)); }
 
 // ---- the lane contract's float helpers (reference kernels/lane.h:17-75) ----
 __device__ inline float lane_exp(float x) {

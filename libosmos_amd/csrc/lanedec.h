@@ -1,0 +1,275 @@
+// libosmos MI355X - the lane contract's per-block arithmetic, shared by the lane kernels (lane.hip) and the fused
+// layer kernels (layer.hip): each type's 32-value block as int8 codes and scale integers (reference kernels/q8.h:28-130,
+// and this build's Q4_0 / Q4_K / Q3_K codes), the block's exact integer half-dots and the contract's float steps
+// (reference kernels/q8.h:133-162, kernels/lane.h:54-68), the lane tree, the input-row rule (kernels/q8.h:164-173).
+#pragma once
+#include "common.h"
+
+namespace osm {
+namespace lane {
+
+static __constant__ Grids kGrids = make_grids();
+
+// a 32-value block's int8 codes: 8 words (4 values each, value 4i + b in byte b of word i); per 8-value chunk k the
+// IQ1 types' delta (+-1, codes 8 grid + delta) or 0; per 16-value half its scale integer s21 (Q2_K, Q4_K: 8 sc) and
+// minimum m8 (8 m); the block scale d and minimum scale dmin. `bias`: a constant subtracted from every code (Q4_0's
+// 8, Q3_K's 4), applied to the integer dot through x's sum - the same integer
+struct Codes {
+  int w[8];
+  int delta[4];
+  int s21[2];
+  int m8[2];
+  float d, dmin;
+};
+
+// 8 unsigned grid bytes, each negated where its sign bit is set: (v ^ m) + (m & 1) a byte, m = 0xFF where negative
+__device__ inline void signed8(uint64_t grid, uint32_t signs, int& lo, int& hi) {
+  uint32_t a = 0, b = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    a |= ((signs >> i) & 1u) * (0xFFu << (8 * i));
+    b |= ((signs >> (4 + i)) & 1u) * (0xFFu << (8 * i));
+  }
+  lo = (int) (((uint32_t) grid ^ a) + (a & 0x01010101u));
+  hi = (int) (((uint32_t) (grid >> 32) ^ b) + (b & 0x01010101u));
+}
+
+__device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <uint32_t T> struct Traits {
+  static constexpr bool iq1 = false, has_min = false, whole = false;
+  static constexpr int bias = 0;  // subtracted from each code
+};
+template <> struct Traits<kIQ1_M> { static constexpr bool iq1 = true, has_min = false, whole = false; static constexpr int bias = 0; };
+template <> struct Traits<kIQ1_S> { static constexpr bool iq1 = true, has_min = false, whole = false; static constexpr int bias = 0; };
+template <> struct Traits<kQ2_K> { static constexpr bool iq1 = false, has_min = true, whole = false; static constexpr int bias = 0; };
+template <> struct Traits<kQ4_0> { static constexpr bool iq1 = false, has_min = false, whole = true; static constexpr int bias = 8; };
+template <> struct Traits<kQ4_K> { static constexpr bool iq1 = false, has_min = true, whole = true; static constexpr int bias = 0; };
+template <> struct Traits<kQ3_K> { static constexpr bool iq1 = false, has_min = false, whole = false; static constexpr int bias = 4; };
+
+// each codebook type's table: its element type and length; `G` below is a pointer to it (constant memory or a
+// workgroup's LDS copy)
+template <uint32_t T> struct GridOf { using E = uint8_t; static constexpr int n = 0; };
+template <> struct GridOf<kIQ2_XXS> { using E = uint64_t; static constexpr int n = 256; };
+template <> struct GridOf<kIQ2_XS> { using E = uint64_t; static constexpr int n = 512; };
+template <> struct GridOf<kIQ2_S> { using E = uint64_t; static constexpr int n = 1024; };
+template <> struct GridOf<kIQ1_S> { using E = uint64_t; static constexpr int n = 2048; };
+template <> struct GridOf<kIQ1_M> { using E = uint64_t; static constexpr int n = 2048; };
+template <> struct GridOf<kIQ3_XXS> { using E = uint32_t; static constexpr int n = 256; };
+
+template <uint32_t T> __device__ inline const typename GridOf<T>::E* const_grid() {
+  if constexpr (T == kIQ2_XXS) return kGrids.iq2xxs;
+  else if constexpr (T == kIQ2_XS) return kGrids.iq2xs;
+  else if constexpr (T == kIQ2_S) return kGrids.iq2s;
+  else if constexpr (T == kIQ1_S || T == kIQ1_M) return kGrids.iq1s;
+  else if constexpr (T == kIQ3_XXS) return kGrids.iq3xxs;
+  else return nullptr;
+}
+
+template <uint32_t T> __device__ void codes(const uint8_t* b, int j, Codes& c, const typename GridOf<T>::E* grid);
+
+// reference kernels/q8.h:46-55
+template <> __device__ inline void codes<kIQ2_XXS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ2_XXS>::E* grid) {
+  const uint8_t* q = b + 2 + 8 * j;
+  const uint32_t aux = ld32(q + 4);
+#pragma unroll
+  for (int k = 0; k < 4; k++) signed8(grid[q[k]], ksign((aux >> (7 * k)) & 0x7F), c.w[2 * k], c.w[2 * k + 1]);
+  c.s21[0] = c.s21[1] = 2 * (int) (aux >> 28) + 1;
+  c.d = f16(ld16(b));
+}
+
+// reference kernels/q8.h:57-66
+template <> __device__ inline void codes<kIQ2_XS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ2_XS>::E* grid) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint32_t q = ld16(b + 2 + 2 * (4 * j + k));
+    signed8(grid[q & 511], ksign(q >> 9), c.w[2 * k], c.w[2 * k + 1]);
+  }
+  const uint32_t s = b[66 + j];
+  c.s21[0] = 2 * (int) (s & 0x0F) + 1, c.s21[1] = 2 * (int) (s >> 4) + 1;
+  c.d = f16(ld16(b));
+}
+
+// reference kernels/q8.h:68-84
+template <> __device__ inline void codes<kIQ1_M>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ1_M>::E* grid) {
+  const uint32_t sc0 = ld32(b + 48), sc1 = ld32(b + 52);
+  const uint64_t sc = (uint64_t) sc0 | (uint64_t) sc1 << 32;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int kk = 4 * j + k;
+    const uint32_t h = (b[32 + kk / 2] >> (4 * (kk % 2))) & 0x0F;
+    const uint64_t g = grid[b[kk] | (h & 0x07) << 8];
+    c.w[2 * k] = (int) (uint32_t) g, c.w[2 * k + 1] = (int) (uint32_t) (g >> 32);
+    c.delta[k] = h & 0x08 ? -1 : 1;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int kk = 4 * j + 2 * h;
+    c.s21[h] = 2 * (int) ((sc >> (16 * (kk / 8) + 3 * ((kk / 2) % 4))) & 0x07) + 1;
+  }
+  const uint32_t s0 = sc0 & 0xFFFF, s1 = sc0 >> 16, s2 = sc1 & 0xFFFF, s3 = sc1 >> 16;
+  c.d = f16((s0 >> 12) | ((s1 >> 8) & 0x00F0) | ((s2 >> 4) & 0x0F00) | (s3 & 0xF000));
+}
+
+// reference kernels/q8.h:86-95
+template <> __device__ inline void codes<kIQ2_S>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ2_S>::E* grid) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int kk = 4 * j + k;
+    signed8(grid[b[2 + kk] | ((b[66 + j] >> (2 * k)) & 0x03) << 8], b[34 + kk], c.w[2 * k], c.w[2 * k + 1]);
+  }
+  const uint32_t s = b[74 + j];
+  c.s21[0] = 2 * (int) (s & 0x0F) + 1, c.s21[1] = 2 * (int) (s >> 4) + 1;
+  c.d = f16(ld16(b));
+}
+
+// reference kernels/q8.h:97-108
+template <> __device__ inline void codes<kIQ3_XXS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ3_XXS>::E* grid) {
+  const uint8_t* q = b + 2 + 8 * j;
+  const uint32_t aux = ld32(b + 66 + 4 * j);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint64_t g = (uint64_t) grid[q[2 * k]] | (uint64_t) grid[q[2 * k + 1]] << 32;
+    signed8(g, ksign((aux >> (7 * k)) & 0x7F), c.w[2 * k], c.w[2 * k + 1]);
+  }
+  c.s21[0] = c.s21[1] = 2 * (2 * (int) (aux >> 28) + 1);
+  c.d = f16(ld16(b));
+}
+
+// reference kernels/q8.h:110-118
+template <> __device__ inline void codes<kQ2_K>(const uint8_t* b, int j, Codes& c, const GridOf<kQ2_K>::E* grid) {
+  const uint8_t* qs = b + 16 + 32 * (j / 4);
+  const int shift = 2 * (j % 4);
+#pragma unroll
+  for (int t = 0; t < 8; t++) c.w[t] = (int) ((ld32(qs + 4 * t) >> shift) & 0x03030303u);
+#pragma unroll
+  for (int h = 0; h < 2; h++) c.s21[h] = 8 * (b[2 * j + h] & 0x0F), c.m8[h] = 8 * (b[2 * j + h] >> 4);
+  c.d = f16(ld16(b + 80)), c.dmin = f16(ld16(b + 82));
+}
+
+// reference kernels/q8.h:120-130
+template <> __device__ inline void codes<kIQ1_S>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ1_S>::E* grid) {
+  const uint32_t h = ld16(b + 34 + 2 * j);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint64_t g = grid[b[2 + 4 * j + k] | ((h >> (3 * k)) & 0x07) << 8];
+    c.w[2 * k] = (int) (uint32_t) g, c.w[2 * k + 1] = (int) (uint32_t) (g >> 32);
+    c.delta[k] = h & 0x8000 ? -1 : 1;
+  }
+  c.s21[0] = c.s21[1] = 2 * (int) ((h >> 12) & 0x07) + 1;
+  c.d = f16(ld16(b));
+}
+
+// build-defined: ggml's Q4_0 (32 values: f16 d, 16 bytes of nibbles; value i < 16 byte i's low nibble, 16 + i its
+// high), codes q - 8 (the 8 through `bias`), one part over the 32 with s21 8 - so d * isum exactly
+template <> __device__ inline void codes<kQ4_0>(const uint8_t* b, int, Codes& c, const GridOf<kQ4_0>::E* grid) {
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const uint32_t v = ld32(b + 2 + 4 * t);
+    c.w[t] = (int) (v & 0x0F0F0F0Fu), c.w[4 + t] = (int) ((v >> 4) & 0x0F0F0F0Fu);
+  }
+  c.s21[0] = c.s21[1] = 8;
+  c.d = f16(ld16(b));
+}
+
+// build-defined: Q4_K's group j (its 6-bit sc and m, reference kernels/quant.h:89-103's layout), codes q, one part
+// with its minimum: ((d * 8 sc) / 8) * isum - ((dmin * 8 m) / 8) * xsum
+template <> __device__ inline void codes<kQ4_K>(const uint8_t* b, int j, Codes& c, const GridOf<kQ4_K>::E* grid) {
+  const uint8_t* s = b + 4;
+  const int sc = j < 4 ? s[j] & 0x3F : (s[j + 4] & 0x0F) | ((s[j - 4] >> 2) & 0x30);
+  const int m = j < 4 ? s[j + 4] & 0x3F : (s[j + 4] >> 4) | ((s[j] >> 2) & 0x30);
+  const uint8_t* qs = b + 16 + (j / 2) * 32;
+  const int sh = 4 * (j % 2);
+#pragma unroll
+  for (int t = 0; t < 8; t++) c.w[t] = (int) ((ld32(qs + 4 * t) >> sh) & 0x0F0F0F0Fu);
+  c.s21[0] = c.s21[1] = 8 * sc, c.m8[0] = c.m8[1] = 8 * m;
+  c.d = f16(ld16(b)), c.dmin = f16(ld16(b + 2));
+}
+
+// build-defined: Q3_K's values 32 j .. 32 j + 31 (reference kernels/quant.h:264-284's layout): codes q2 + 4 h - 4
+// (the 4 through `bias`), two halves, each s21 = 8 (sc - 32) of its 16-value group
+template <> __device__ inline void codes<kQ3_K>(const uint8_t* b, int j, Codes& c, const GridOf<kQ3_K>::E* grid) {
+  const int n = j / 4, jj = j % 4;
+  const uint8_t* qs = b + 32 + 32 * n;
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    const uint32_t q2 = (ld32(qs + 4 * t) >> (2 * jj)) & 0x03030303u;
+    const uint32_t hb = (ld32(b + 4 * t) >> (4 * n + jj)) & 0x01010101u;
+    c.w[t] = (int) (q2 + (hb << 2));
+  }
+  const uint8_t* sc = b + 96;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int g = 2 * j + h, grp = g / 4, w = g % 4;
+    const int low = ((grp & 1 ? sc[4 + w] : sc[w]) >> (grp & 2 ? 4 : 0)) & 0x0F;
+    const int sc6 = low | ((sc[8 + w] >> (2 * grp)) & 0x03) << 4;
+    c.s21[h] = 8 * (sc6 - 32);
+  }
+  c.d = f16(ld16(b + 108));
+}
+
+// the block's contribution before x's scale (reference kernels/q8.h:133-162)
+template <uint32_t T>
+__device__ inline float block_sum(const Codes& c, const int* x) {
+  using Tr = Traits<T>;
+  int isum[2], xsum[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    int s = 0, sx = 0;
+#pragma unroll
+    for (int k = 2 * h; k < 2 * h + 2; k++) {
+      const int gx = dot4(c.w[2 * k + 1], x[2 * k + 1], dot4(c.w[2 * k], x[2 * k], 0));
+      if constexpr (Tr::iq1 || Tr::has_min || Tr::bias) {
+        const int xk = dot4(0x01010101, x[2 * k + 1], dot4(0x01010101, x[2 * k], 0));
+        if constexpr (Tr::iq1) s += 8 * gx + c.delta[k] * xk;
+        else s += gx - Tr::bias * xk;
+        sx += xk;
+      } else {
+        s += gx;
+      }
+    }
+    isum[h] = s, xsum[h] = sx;
+  }
+  if constexpr (Tr::whole) {
+    const int is = isum[0] + isum[1];
+    if constexpr (Tr::has_min)
+      return __fsub_rn(lane_part(c.d, c.s21[0], is), lane_part(c.dmin, c.m8[0], xsum[0] + xsum[1]));
+    else
+      return lane_part(c.d, c.s21[0], is);
+  } else if constexpr (Tr::has_min) {
+    const float p0 = __fsub_rn(lane_part(c.d, c.s21[0], isum[0]), lane_part(c.dmin, c.m8[0], xsum[0]));
+    const float p1 = __fsub_rn(lane_part(c.d, c.s21[1], isum[1]), lane_part(c.dmin, c.m8[1], xsum[1]));
+    return __fadd_rn(p0, p1);
+  } else {
+    return __fadd_rn(lane_part(c.d, c.s21[0], isum[0]), lane_part(c.d, c.s21[1], isum[1]));
+  }
+}
+
+// a launch's NT input rows for output rows r0 .. r0 + NT - 1 (reference kernels/q8.h:164-173): row r's own (xin
+// NULL), else row xin[r]; the rows past the count read as the count's last - summed, never stored
+template <int NT>
+__device__ inline void in_rows(const int32_t* xin, uint32_t r0, uint32_t cnt, uint64_t* xr) {
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const uint32_t r = r0 + ((uint32_t) t < cnt ? (uint32_t) t : cnt - 1);
+    xr[t] = xin ? (uint64_t) (uint32_t) xin[r] : r;
+  }
+}
+
+__device__ inline void load_x(const int8_t* q, uint64_t at, int* x) {
+  const int4* xp = (const int4*) (q + at);
+  const int4 a = xp[0], b = xp[1];
+  x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+}
+
+// the lanes' xor tree over the row's L logical lanes: acc[l] + acc[l ^ o], o = L/2 .. 1 (reference kernels/q8.h:209)
+template <int L>
+__device__ inline float tree(float v) {
+#pragma unroll
+  for (int o = L / 2; o > 0; o >>= 1) v = __fadd_rn(v, xor_lane(v, o));
+  return v;
+}
+
+
+}  // namespace lane
+}  // namespace osm

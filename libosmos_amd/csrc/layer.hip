@@ -1,66 +1,103 @@
 // libosmos MI355X - one routed MoE layer over the lane's int8 contract (include/osmos_mi355x.h: osmos_lane_layer,
-// osmos_lane_workspace): host code sequencing the library's own entry points on one stream, the order of the reference's
-// src/run/hip_lane.c:115-222 (fwd_lane_experts) with its host-side tables replaced by osmos_lane_tables (device), so a
-// step needs no host round trip and can be captured in a HIP graph.
-#include "common.h"
+// osmos_lane_workspace): two fused launches (fused.h) - gate/up with the activation, then down with the tokens'
+// ordered expert sums - in the order of the reference's src/run/hip_lane.c:115-222 and src/cpu/lane.c:98-118, so every
+// output is the reference CPU lane's bits. no host round trip, no allocation: capturable in a HIP graph.
+#include "fused.h"
 
 extern "C" {
 #include "../../include/osmos_mi355x.h"
 }
 
-namespace {
+namespace osm {
+namespace layer {
 
-constexpr uint64_t kAlign = 256;
-inline uint64_t up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+using fused::DnArgs;
+using fused::GuArgs;
 
-// the workspace's pieces, in order
-struct Carve {
-  uint64_t q, qd, tok, pair, cnt, xrow, wg, wu, wd, order, h, qh, qhd, ye, total;
-};
-
-Carve carve(const OsmosLaneLayer* L, uint32_t n_tok) {
-  const uint64_t n = (uint64_t) n_tok * L->k;
-  Carve c;
-  uint64_t at = 0;
-  auto take = [&](uint64_t bytes) { const uint64_t r = at; at += up(bytes); return r; };
-  c.q = take((uint64_t) n_tok * L->dim), c.qd = take((uint64_t) n_tok * (L->dim / 32) * 4);
-  c.tok = take(n * 4), c.pair = take(n * 4), c.cnt = take(n * 4), c.xrow = take(n * 4);
-  c.wg = take(n * 8), c.wu = take(n * 8), c.wd = take(n * 8), c.order = take(n * 4);
-  c.h = take(n * L->ff * 4), c.qh = take(n * L->ff), c.qhd = take(n * (L->ff / 32) * 4);
-  c.ye = take(n * L->dim * 4);
-  c.total = at;
-  return c;
+template <uint32_t T, int NT, int L>
+bool gu_launch(const GuArgs& a, hipStream_t s) {
+  const uint32_t n = a.n_tok * a.k;
+  const fused::GuLds l = fused::gu_lds((uint32_t) row_bytes<T>(a.dim), a.dim, NT, fused::grid_bytes<T>(), n);
+  if (l.total > 160 * 1024) return false;
+  auto k = fused::gu_kernel<T, NT, L>;
+  if (l.total > 64 * 1024 &&
+      hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
+    return false;
+  k<<<dim3(a.ff / fused::kGuRows, n), fused::kThreads, l.total, s>>>(a);
+  return hipGetLastError() == hipSuccess;
 }
 
-}  // namespace
+template <uint32_t T, int L>
+bool dn_launch(const DnArgs& a, hipStream_t s) {
+  const fused::DnLds l = fused::dn_lds((uint32_t) row_bytes<T>(a.ff), a.ff, a.k, fused::grid_bytes<T>());
+  if (l.total > 160 * 1024) return false;
+  auto k = fused::dn_kernel<T, L>;
+  if (l.total > 64 * 1024 &&
+      hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
+    return false;
+  k<<<dim3(a.dim / fused::kDnRows, a.n_tok), fused::kThreads, l.total, s>>>(a);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <uint32_t T>
+bool gu_by(const GuArgs& a, hipStream_t s) {
+  if (a.dim % Block<T>::values) return false;
+  const bool wide = a.dim >= 4096;  // the contract's 32 lanes a row
+  if (a.n_tok == 1) return wide ? gu_launch<T, 1, 32>(a, s) : gu_launch<T, 1, 16>(a, s);
+  return wide ? gu_launch<T, 2, 32>(a, s) : gu_launch<T, 2, 16>(a, s);
+}
+
+template <uint32_t T>
+bool dn_by(const DnArgs& a, hipStream_t s) {
+  if (a.ff % Block<T>::values) return false;
+  return a.ff >= 4096 ? dn_launch<T, 32>(a, s) : dn_launch<T, 16>(a, s);
+}
+
+#define OSM_LANE_TYPES(X) X(kIQ2_XXS) X(kIQ2_XS) X(kIQ1_M) X(kIQ1_S) X(kIQ2_S) X(kIQ3_XXS) X(kQ2_K) X(kQ4_0) X(kQ4_K) X(kQ3_K)
+
+bool gu(uint32_t type, const GuArgs& a, hipStream_t s) {
+  switch (type) {
+#define X(t) \
+  case t: return gu_by<t>(a, s);
+    OSM_LANE_TYPES(X)
+#undef X
+    default: return false;
+  }
+}
+
+bool dn(uint32_t type, const DnArgs& a, hipStream_t s) {
+  switch (type) {
+#define X(t) \
+  case t: return dn_by<t>(a, s);
+    OSM_LANE_TYPES(X)
+#undef X
+    default: return false;
+  }
+}
+
+}  // namespace layer
+}  // namespace osm
+
+using namespace osm;
 
 extern "C" OSM_API uint64_t osmos_lane_workspace(const OsmosLaneLayer* L, uint32_t n_tok) {
   if (!L || !n_tok || !L->k) return 0;
-  return carve(L, n_tok).total;
+  return ((uint64_t) n_tok * L->k * L->ff * 4 + 255) / 256 * 256;  // h: a row of ff a pick
 }
 
 extern "C" OSM_API bool osmos_lane_layer(const OsmosLaneLayer* L, const float* x, uint32_t n_tok, const int32_t* ids,
                                          const float* w, const float* add, float* out, void* workspace,
                                          uint64_t workspace_bytes, void* stream) {
-  if (!L || !x || !n_tok || !ids || !w || !add || !out || !workspace || !L->k || !L->dim || !L->ff ||
-      (uintptr_t) workspace % kAlign || (uint64_t) n_tok * L->k > OSMOS_LANE_MAX_PAIRS)
+  if (!L || !x || !n_tok || !ids || !w || !add || !out || !workspace || !L->k || !L->dim || !L->ff || !L->n_exp ||
+      !L->gate || !L->up || !L->down || n_tok > fused::kMaxTok || L->k > fused::kMaxK || L->dim % 32 ||
+      L->ff % fused::kGuRows || L->ff % 32 || L->dim % fused::kDnRows || (uintptr_t) workspace % 16 ||
+      ((uintptr_t) L->gate | (uintptr_t) L->up | (uintptr_t) L->down | L->gate_bytes | L->up_bytes | L->down_bytes) % 16)
     return false;
-  const Carve c = carve(L, n_tok);
-  if (workspace_bytes < c.total) return false;
-  uint8_t* ws = (uint8_t*) workspace;
-  int8_t *q = (int8_t*) (ws + c.q), *qh = (int8_t*) (ws + c.qh);
-  float *qd = (float*) (ws + c.qd), *h = (float*) (ws + c.h), *qhd = (float*) (ws + c.qhd), *ye = (float*) (ws + c.ye);
-  int32_t *tok = (int32_t*) (ws + c.tok), *pair = (int32_t*) (ws + c.pair), *cnt = (int32_t*) (ws + c.cnt);
-  int32_t *xrow = (int32_t*) (ws + c.xrow), *order = (int32_t*) (ws + c.order);
-  const void **wg = (const void**) (ws + c.wg), **wu = (const void**) (ws + c.wu), **wd = (const void**) (ws + c.wd);
-  const uint32_t n = n_tok * L->k, max_cnt = n_tok < MV_MAX_TOKENS ? n_tok : MV_MAX_TOKENS;
-  const void* base[3] = {L->gate, L->up, L->down};
-  const uint64_t bytes[3] = {L->gate_bytes, L->up_bytes, L->down_bytes};
-  return q8_round(x, n_tok, L->dim, L->dim, q, qd, stream) &&
-         osmos_lane_tables(ids, n_tok, L->k, L->n_exp, base, bytes, tok, pair, cnt, xrow, wg, wu, wd, order, stream) &&
-         q8_gate_up(L->type_gu, wg, wu, cnt, xrow, tok, pair, n, max_cnt, L->ff, L->dim, q, qd, w, L->lim, h, L->ff,
-                    stream) &&
-         q8_round(h, n, L->ff, L->ff, qh, qhd, stream) &&
-         q8_group_tok(L->type_down, wd, cnt, xrow, nullptr, n, max_cnt, L->dim, L->ff, qh, qhd, ye, L->dim, stream) &&
-         ops_gather_sum_add(out, ye, order, L->k, n_tok, L->dim, add, stream);
+  if (workspace_bytes < osmos_lane_workspace(L, n_tok)) return false;
+  float* h = (float*) workspace;
+  const hipStream_t s = (hipStream_t) stream;
+  const fused::GuArgs ga = {x, ids, w, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->gate, (const uint8_t*) L->up,
+                            L->gate_bytes, L->up_bytes, L->lim, h};
+  const fused::DnArgs da = {h, ids, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->down, L->down_bytes, add, out};
+  return layer::gu(L->type_gu, ga, s) && layer::dn(L->type_down, da, s);
 }

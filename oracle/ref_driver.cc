@@ -2,6 +2,7 @@
 // vectors (tests/golden/make_golden.py) and bench.py's CPU baseline. this file is this repository's; what it calls
 // is the reference's src/cpu/q8.c (built as C++, so its functions have C++ linkage here) and src/cpu/expert.c (C).
 #include <pthread.h>
+#include <cmath>
 #include <cstdint>
 
 #include "lane.h"
@@ -66,6 +67,94 @@ bool ref_q8_rows_mt(uint32_t type, const void *w, uint32_t cols, uint32_t rows, 
   bool ok = true;
   for (int i = 0; i < threads; i++) pthread_join(th[i], nullptr), ok = ok && sh[i].ok;
   return ok;
+}
+
+// one bs-n lane layer's experts on `threads` host threads (the CPU baseline): the reference's cpu_q8_rows over each
+// phase's rows split evenly (src/cpu/lane.c:53-57's share, 98-118's phases: gate/up + lane_swiglu, the activations
+// rounded, down), a barrier between phases. expert e's gate/up/down at g[e], u[e], dn[e], over rows r0[e] .. + cnt[e]
+// of q / d (x rounded); y rows of dim. the threads are created once and run `reps` layers back to back.
+struct Layer {
+  uint32_t type, dim, ff, n_e, n_rows;
+  const void *const *g, *const *u, *const *dn;
+  const uint32_t *r0, *cnt;
+  const int8_t *q;
+  const float *d, *scale;
+  float *gs, *us, *h, *hd, *y;
+  int8_t *hq;
+  int threads, reps;
+  pthread_barrier_t bar;
+  bool ok;
+};
+
+struct Worker {
+  Layer *L;
+  int id;
+};
+
+static void span(uint64_t total, int id, int n, uint64_t *a, uint64_t *b)
+{
+  *a = total * (uint64_t)id / (uint64_t)n, *b = total * (uint64_t)(id + 1) / (uint64_t)n;
+}
+
+static void *layer_worker(void *p)
+{
+  Worker *w = (Worker *)p;
+  Layer *L = w->L;
+  const uint32_t D = L->dim, F = L->ff;
+  for (int rep = 0; rep < L->reps; rep++) {
+    uint64_t a, b;
+    span((uint64_t)L->n_e * F, w->id, L->threads, &a, &b);  // gate / up rows of all experts end to end
+    for (uint32_t e = 0; e < L->n_e; e++) {
+      const uint64_t lo = (uint64_t)e * F, r0 = a > lo ? a - lo : 0, r1 = b < lo + F ? b - lo : F;
+      if (r0 >= r1 || lo >= b) continue;
+      const uint64_t row = L->r0[e];
+      if (!cpu_q8_rows(L->type, L->g[e], D, (uint32_t)r0, (uint32_t)r1, L->q + row * D, L->d + row * (D / 32),
+                       L->cnt[e], L->gs + row * F, F) ||
+          !cpu_q8_rows(L->type, L->u[e], D, (uint32_t)r0, (uint32_t)r1, L->q + row * D, L->d + row * (D / 32),
+                       L->cnt[e], L->us + row * F, F))
+        L->ok = false;
+      for (uint32_t t = 0; t < L->cnt[e]; t++)
+        for (uint64_t r = r0; r < r1; r++) {
+          const uint64_t i = (row + t) * F + r;
+          L->h[i] = lane_swiglu(L->gs[i], L->us[i], INFINITY, L->scale[row + t]);
+        }
+    }
+    pthread_barrier_wait(&L->bar);
+    for (uint32_t r = (uint32_t)w->id; r < L->n_rows; r += (uint32_t)L->threads)
+      if (!cpu_q8_round(L->h + (uint64_t)r * F, 1, F, F, L->hq + (uint64_t)r * F, L->hd + (uint64_t)r * (F / 32)))
+        L->ok = false;
+    pthread_barrier_wait(&L->bar);
+    span((uint64_t)L->n_e * D, w->id, L->threads, &a, &b);
+    for (uint32_t e = 0; e < L->n_e; e++) {
+      const uint64_t lo = (uint64_t)e * D, r0 = a > lo ? a - lo : 0, r1 = b < lo + D ? b - lo : D;
+      if (r0 >= r1 || lo >= b) continue;
+      const uint64_t row = L->r0[e];
+      if (!cpu_q8_rows(L->type, L->dn[e], F, (uint32_t)r0, (uint32_t)r1, L->hq + row * F, L->hd + row * (F / 32),
+                       L->cnt[e], L->y + row * D, D))
+        L->ok = false;
+    }
+    pthread_barrier_wait(&L->bar);
+  }
+  return nullptr;
+}
+
+bool ref_lane_layer_mt(uint32_t type, uint32_t dim, uint32_t ff, const void *const *g, const void *const *u,
+                       const void *const *dn, const uint32_t *r0, const uint32_t *cnt, uint32_t n_e, uint32_t n_rows,
+                       const int8_t *q, const float *d, const float *scale, float *y, int threads, int reps)
+{
+  if (threads < 1 || threads > 256 || reps < 1) return false;
+  Layer L = {type, dim, ff, n_e, n_rows, g, u, dn, r0, cnt, q, d, scale, nullptr, nullptr, nullptr, nullptr, y,
+             nullptr, threads, reps, {}, true};
+  L.gs = new float[(size_t)n_rows * ff], L.us = new float[(size_t)n_rows * ff], L.h = new float[(size_t)n_rows * ff];
+  L.hd = new float[(size_t)n_rows * (ff / 32)], L.hq = new int8_t[(size_t)n_rows * ff];
+  pthread_barrier_init(&L.bar, nullptr, (unsigned)threads);
+  pthread_t th[256];
+  Worker w[256];
+  for (int i = 0; i < threads; i++) w[i] = Worker{&L, i}, pthread_create(&th[i], nullptr, layer_worker, &w[i]);
+  for (int i = 0; i < threads; i++) pthread_join(th[i], nullptr);
+  pthread_barrier_destroy(&L.bar);
+  delete[] L.gs, delete[] L.us, delete[] L.h, delete[] L.hd, delete[] L.hq;
+  return L.ok;
 }
 
 }  // extern "C"

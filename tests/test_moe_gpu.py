@@ -222,3 +222,29 @@ def test_lane_layer_qwen_shape(g, n_tok):
         for t in (0, n_tok - 1):
             L.forward(g.dev(x[t:t + 1]), g.dev(ids[t:t + 1]), g.dev(wts[t:t + 1]), torch.zeros((1, dim), device="cuda"), one)
             assert (g.bits(g.host(one)[0]) == g.bits(want[t])).all()
+
+
+@pytest.mark.parametrize("name", ["IQ1_S", "IQ1_M", "IQ2_XXS"])
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_lane_layer_deepseek_shape(g, name, n_tok):
+    """the DeepSeek-style expert shape (hidden 7168, expert ff 2048: 32 lanes a gate/up row, 16 a down row), top-9
+    (8 routed + the shared one as a ninth pick) over 24 experts: the oracle's bits"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t = synth.ID[name]
+    n_exp, k, dim, ff = 24, 9, 7168, 2048
+    rng = np.random.default_rng(50 + n_tok)
+    gate = [synth.iq_blocks(t, ff, dim, 100 + e) for e in range(n_exp)]
+    up = [synth.iq_blocks(t, ff, dim, 200 + e) for e in range(n_exp)]
+    down = [synth.iq_blocks(t, dim, ff, 300 + e) for e in range(n_exp)]
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids = np.stack([np.concatenate([rng.choice(n_exp - 1, k - 1, replace=False), [n_exp - 1]]) for _ in range(n_tok)])
+    ids = ids.astype(np.int32)
+    wts = rng.uniform(0.01, 0.3, (n_tok, k)).astype(np.float32)
+    want = _lane_layer_oracle(t, x, ids, wts, gate, up, down, dim, ff, math.inf)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(t, t, dim, ff, n_exp, k, D(gate), D(up), D(down))
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("deepseek layer", name, n_tok, flush=True)
+    L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
