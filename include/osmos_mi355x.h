@@ -34,7 +34,9 @@ bool osmos_lane_tables(const int32_t *ids, uint32_t n_tok, uint32_t k, uint32_t 
    ascending expert id and add[t] added after (ops_gather_sum_add) into out (n_tok rows of dim). the bits of the
    reference CPU lane for every token, whatever n_tok. `gate`, `up`, `down`: each tensor's n_exp experts back to back,
    an expert `*_bytes` apart (GGUF rows: gate/up ff rows of dim, down dim rows of ff); ids / w: the router's n_tok x k
-   picks and weights. workspace: device memory of osmos_lane_workspace bytes (256-aligned), the caller's. */
+   picks and weights. workspace: device memory of osmos_lane_workspace bytes (256-aligned), the caller's, zeroed once
+   before its first use (every call leaves its control words zeroed again); calls sharing a workspace must be ordered
+   on one stream. */
 typedef struct OsmosLaneLayer
 {
   uint32_t type_gu, type_down; /* the lane's types (q8.h) */

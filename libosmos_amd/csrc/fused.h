@@ -10,6 +10,8 @@
 //   (q8_round's bits), stages the k experts' tile rows, sums each (expert, row) in the lane order, then each row's k
 //   sums in ascending expert id (the reference's ops_gather_sum_add order) and add[t][row] after.
 #pragma once
+#include <type_traits>
+
 #include "lanedec.h"
 
 namespace osm {
@@ -17,14 +19,14 @@ namespace fused {
 
 using namespace lane;
 
-constexpr int kThreads = 256, kWaves = 4;
+constexpr int kThreads = 1024, kWaves = kThreads / 64;
 constexpr uint32_t kGuRows = 16, kDnRows = 8, kMaxTok = 64, kMaxK = 32;
 
 __host__ __device__ constexpr uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
 // gu_kernel's LDS: the gate and up tiles, NT tokens' int8 x and scales, the codebook, the expert's tokens
 struct GuLds {
-  uint32_t wg, wu, q, d, grid, toks, ids, total;
+  uint32_t wg, wu, q, d, grid, toks, ids, subs, gv, total;
 };
 __host__ __device__ inline GuLds gu_lds(uint32_t row_bytes, uint32_t dim, int nt, uint32_t grid_bytes, uint32_t n) {
   GuLds l;
@@ -36,13 +38,15 @@ __host__ __device__ inline GuLds gu_lds(uint32_t row_bytes, uint32_t dim, int nt
   l.grid = at, at += align16(grid_bytes);
   l.toks = at, at += align16((2 * kMaxTok + 1) * 4);
   l.ids = at, at += align16(n * 4);
+  l.subs = at, at += align16(2 * (uint32_t) nt * kGuRows * (dim / 32) * 4);
+  l.gv = at, at += align16(2 * (uint32_t) nt * kGuRows * 4);
   l.total = at;
   return l;
 }
 
 // dn_kernel's LDS: the k experts' tiles, the k rounded h rows and scales, the k row sums, the sorted picks
 struct DnLds {
-  uint32_t w, q, d, grid, ye, picks, total;
+  uint32_t w, q, d, grid, ye, picks, subs, total;
 };
 __host__ __device__ inline DnLds dn_lds(uint32_t row_bytes, uint32_t ff, uint32_t k, uint32_t grid_bytes) {
   DnLds l;
@@ -53,6 +57,7 @@ __host__ __device__ inline DnLds dn_lds(uint32_t row_bytes, uint32_t ff, uint32_
   l.grid = at, at += align16(grid_bytes);
   l.ye = at, at += align16(k * kDnRows * 4);
   l.picks = at, at += align16(2 * kMaxK * 4);
+  l.subs = at, at += align16(k * kDnRows * (ff / 32) * 4);
   l.total = at;
   return l;
 }
@@ -84,27 +89,48 @@ struct DnArgs {
 // issues every thread's 16-byte loads of the current round (up to kPer a thread: the weights of a tile fit one round),
 // store() writes them to LDS. segment j (per_seg 16-byte words) comes from src(j) and lands at lds + j * per_seg * 16:
 // the destination is the word's linear index, the source found by a reciprocal (exact: checked and corrected)
-constexpr int kPer = 16;
+constexpr int kPer = 4;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (native vectors: kept in registers across waits)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 struct Staged {
-  uint4 v[kPer];
+  u32x4 v0, v1, v2, v3;
+  template <int U>
+  __device__ __forceinline__ u32x4& at() {
+    static_assert(U >= 0 && U < kPer);
+    if constexpr (U == 0) return v0;
+    else if constexpr (U == 1) return v1;
+    else if constexpr (U == 2) return v2;
+    else return v3;
+  }
+  template <int U>
+  __device__ __forceinline__ const u32x4& at() const {
+    return const_cast<Staged*>(this)->at<U>();
+  }
 };
+// f(integral_constant<int, u>) for u = 0 .. N - 1, unrolled at compile time (constant indices keep the staged words
+// in registers)
+template <int N, int U = 0, typename F>
+__device__ __forceinline__ void unroll(F&& f) {
+  if constexpr (U < N) {
+    f(std::integral_constant<int, U>());
+    unroll<N, U + 1>(f);
+  }
+}
 template <typename Src>
-__device__ inline void stage_load(Staged& st, Src src, uint32_t n, uint32_t per_seg, float inv, uint32_t base) {
-#pragma unroll
-  for (int u = 0; u < kPer; u++) {
-    const uint32_t l0 = base + u * kThreads + threadIdx.x, l = l0 < n ? l0 : 0;  // (past the end: word 0 again)
+__device__ __forceinline__ void stage_load(Staged& st, Src src, uint32_t n, uint32_t per_seg, float inv, uint32_t base) {
+  unroll<kPer>([&](auto u) __attribute__((always_inline)) {
+    const uint32_t l0 = base + u.value * kThreads + threadIdx.x, l = l0 < n ? l0 : 0;  // (past the end: word 0 again)
     uint32_t j = (uint32_t) ((float) l * inv);
     j -= j * per_seg > l;
     j += (j + 1) * per_seg <= l;
-    st.v[u] = ((const uint4*) src(j))[l - j * per_seg];
-  }
+    st.template at<u.value>() = ((const u32x4*) src(j))[l - j * per_seg];
+  });
 }
-__device__ inline void stage_store(const Staged& st, uint8_t* lds, uint32_t n, uint32_t base) {
-#pragma unroll
-  for (int u = 0; u < kPer; u++) {
-    const uint32_t l = base + u * kThreads + threadIdx.x;
-    if (l < n) ((uint4*) lds)[l] = st.v[u];
-  }
+__device__ __forceinline__ void stage_store(const Staged& st, uint8_t* lds, uint32_t n, uint32_t base) {
+  unroll<kPer>([&](auto u) __attribute__((always_inline)) {
+    const uint32_t l = base + u.value * kThreads + threadIdx.x;
+    if (l < n) ((u32x4*) lds)[l] = st.template at<u.value>();
+  });
 }
 
 // rows of 32-value blocks rounded to int8 as q8_round rounds them (reference kernels/q8.h:263-277): 8 threads a
@@ -112,28 +138,39 @@ __device__ inline void stage_store(const Staged& st, uint8_t* lds, uint32_t n, u
 // order), each value's code, the 4 codes one word. round_load() issues a round of up to kRPer float4 loads a thread
 // (block base + threadIdx.x / 8 + 32 u), round_store() reduces and writes them; value(blk, c) is the address of block
 // blk's value c
-constexpr int kRPer = 8;
+constexpr int kRPer = 2;
 constexpr uint32_t kRoundBlocks = (kThreads / 8) * kRPer;  // blocks a round
 struct Rounded {
-  float4 v[kRPer];
-};
-template <typename Val>
-__device__ inline void round_load(Rounded& r, Val value, uint32_t blocks, uint32_t base) {
-  const uint32_t g = threadIdx.x / 8, c = 4 * (threadIdx.x % 8);
-#pragma unroll
-  for (int u = 0; u < kRPer; u++) {
-    const uint32_t blk = base + g + (kThreads / 8) * u;
-    r.v[u] = *(const float4*) value(blk < blocks ? blk : 0, c);
+  f32x4 v0, v1;
+  template <int U>
+  __device__ __forceinline__ f32x4& at() {
+    static_assert(U >= 0 && U < kRPer);
+    if constexpr (U == 0) return v0;
+    else return v1;
   }
+  template <int U>
+  __device__ __forceinline__ const f32x4& at() const {
+    return const_cast<Rounded*>(this)->at<U>();
+  }
+};
+__device__ inline f32x4 load_coherent4(const float* p);
+template <bool Coherent = false, typename Val>
+__device__ __forceinline__ void round_load(Rounded& r, Val value, uint32_t blocks, uint32_t base) {
+  const uint32_t g = threadIdx.x / 8, c = 4 * (threadIdx.x % 8);
+  unroll<kRPer>([&](auto u) __attribute__((always_inline)) {
+    const uint32_t blk = base + g + (kThreads / 8) * u.value;
+    const float* p = value(blk < blocks ? blk : 0, c);
+    if constexpr (Coherent) r.template at<u.value>() = load_coherent4(p);
+    else r.template at<u.value>() = *(const f32x4*) p;
+  });
 }
 __device__ inline uint32_t q8_byte(float v, float inv) { return (uint32_t) ((int) rintf(__fmul_rn(v, inv)) & 0xFF); }
-__device__ inline void round_store(const Rounded& r, uint32_t blocks, uint32_t base, uint32_t nb_row, uint32_t cols,
+__device__ __forceinline__ void round_store(const Rounded& r, uint32_t blocks, uint32_t base, uint32_t nb_row, uint32_t cols,
                                    int8_t* q, float* d) {
   const uint32_t g = threadIdx.x / 8, c = 4 * (threadIdx.x % 8);
-#pragma unroll
-  for (int u = 0; u < kRPer; u++) {
-    const uint32_t blk = base + g + (kThreads / 8) * u;
-    const float4 v = r.v[u];
+  unroll<kRPer>([&](auto u) __attribute__((always_inline)) {
+    const uint32_t blk = base + g + (kThreads / 8) * u.value;
+    const f32x4 v = r.template at<u.value>();
     float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     am = fmaxf(am, xor_lane(am, 1));
     am = fmaxf(am, xor_lane(am, 2));
@@ -145,17 +182,17 @@ __device__ inline void round_store(const Rounded& r, uint32_t blocks, uint32_t b
           q8_byte(v.x, inv) | q8_byte(v.y, inv) << 8 | q8_byte(v.z, inv) << 16 | q8_byte(v.w, inv) << 24;
       if (c == 0) d[blk] = __fdiv_rn(am, 127.0f);
     }
-  }
+  });
 }
 
 
 // the codebook, copied by the first threads of a workgroup (1 - 16 KB of constant memory, 16-aligned)
 template <uint32_t T>
-__device__ inline void grid_copy(uint8_t* lds) {
+__device__ __forceinline__ void grid_copy(uint8_t* lds) {
   if constexpr (grid_bytes<T>() > 0) {
     constexpr uint32_t n = grid_bytes<T>() / 16;
-    const uint4* src = (const uint4*) const_grid<T>();
-    uint4 v[(n + kThreads - 1) / kThreads];
+    const u32x4* src = (const u32x4*) const_grid<T>();
+    u32x4 v[(n + kThreads - 1) / kThreads];
 #pragma unroll
     for (uint32_t u = 0; u < (n + kThreads - 1) / kThreads; u++) {
       const uint32_t l = u * kThreads + threadIdx.x;
@@ -164,40 +201,89 @@ __device__ inline void grid_copy(uint8_t* lds) {
 #pragma unroll
     for (uint32_t u = 0; u < (n + kThreads - 1) / kThreads; u++) {
       const uint32_t l = u * kThreads + threadIdx.x;
-      if (l < n) ((uint4*) lds)[l] = v[u];
+      if (l < n) ((u32x4*) lds)[l] = v[u];
     }
   }
 }
 
-template <uint32_t T, int NT, int L>
-__global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+// the kernels' compute is in two phases. A: every (matrix, row, block) of the tile gets its block's `sub` (the codes,
+// the exact integer half-dots, the contract's float parts: block_sum) from any thread, into LDS - the bulk of the work,
+// spread over all the waves; items are ordered so that a wave's lanes share a block index (its x words read once for
+// all of them). B: each row's logical lanes run the contract's chain, acc = fmaf(xd[s], sub[s], acc) over their blocks
+// s = ll, ll + L, ... in order, and the lanes' xor tree - the same values in the same order as the reference's
+// per-lane loop, so the same bits.
+
+// the single launch's hand-off of h between workgroups (layer_kernel). h is written and read with device-coherent
+// accesses (agent-scope atomics: they write through and read past the XCDs' own L2s), so no cache-wide write-back or
+// invalidate is needed: a writer waits for its stores to complete (vmcnt 0) before its tile's counter is raised, and
+// a reader reads h only after it has seen the counter. the control words live in the caller's workspace, zeroed
+// before the first use; every launch leaves them zeroed.
+constexpr uint32_t kExitGroups = 64;  // exit counters (one single counter would serialize every workgroup's atomic)
+constexpr uint32_t kCtrlStride = 16;  // words between counters (a 64-byte line each)
+constexpr uint32_t kFlagCopies = 16;  // a token's ready flag, in as many lines (its down tiles poll one each)
+struct Ctrl {
+  uint32_t top, error, pad[kCtrlStride - 2];  // the groups that have left; a sticky error
+  uint32_t exited[kExitGroups][kCtrlStride];  // [g][0]: workgroups of group g (blockIdx % 64) that have left
+  // then, a line each: [n picks] each pick's finished gate/up tiles; [n_tok] each token's finished picks;
+  // [n_tok][kFlagCopies] each token's ready flag (all its picks' h written)
+};
+__host__ __device__ inline uint32_t* done_of(Ctrl* c) { return reinterpret_cast<uint32_t*>(c + 1); }
+__host__ __device__ inline uint64_t ctrl_lines(uint32_t n, uint32_t n_tok) { return n + n_tok + (uint64_t) n_tok * kFlagCopies; }
+constexpr uint32_t kSpinMax = 1u << 18;  // a down tile's wait for its picks, at most (then the error is set and it
+                                         // goes on: every wave reaches its end)
+
+// the lanes' tree over a run-time lane count (16 or 32; uniform across the wave)
+__device__ inline float tree_rt(float v, int L) { return L == 32 ? tree<32>(v) : tree<16>(v); }
+
+__device__ inline void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline f32x4 load_coherent4(const float* p) {
+  const uint64_t lo = __hip_atomic_load((const uint64_t*) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load((const uint64_t*) p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  f32x4 v;
+  v.x = __uint_as_float((uint32_t) lo), v.y = __uint_as_float((uint32_t) (lo >> 32));
+  v.z = __uint_as_float((uint32_t) hi), v.w = __uint_as_float((uint32_t) (hi >> 32));
+  return v;
+}
+// this wave's memory operations complete (the compiler moves no memory access across it)
+__device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// one gate/up tile: expert of pick m (its first pick's tile: others return at once), rows tile * 16 .. + 16; with
+// `done` (the single launch's control lines), the covered picks' counters are raised once its h rows are written
+template <uint32_t T, int NT>
+__device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t tile, uint8_t* smem, uint32_t* done, int L) {
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
-  const uint32_t m = blockIdx.y, r0 = blockIdx.x * kGuRows, n = a.n_tok * a.k;
+  const uint32_t r0 = tile * kGuRows, n = a.n_tok * a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
   const GuLds L_ = gu_lds(rb, a.dim, NT, grid_bytes<T>(), n);
-  int32_t* ids = (int32_t*) (smem + L_.ids);
-  int32_t* toks = (int32_t*) (smem + L_.toks);  // [0, kMaxTok): the expert's picks in token order; [kMaxTok + t]:
-                                                 // token t's pick of it or -1; [2 kMaxTok]: their count
-  for (uint32_t i = threadIdx.x; i < n; i += kThreads) ids[i] = a.ids[i];
-  __syncthreads();
-  const int32_t e = ids[m];
-  // the expert's first pick owns the workgroup; the others leave (the same decision in every thread)
-  int dup = 0;
-  for (uint32_t j = threadIdx.x; j < m; j += kThreads) dup |= ids[j] == e;
-  if (__syncthreads_or(dup)) return;
-  if (threadIdx.x < kWave) {  // wave 0, a lane a token: its pick of this expert if any (a token's picks are distinct
-                              // experts), placed by the count of earlier tokens that picked it (token order)
-    int32_t p = -1;
-    if (threadIdx.x < a.n_tok)
-      for (uint32_t j = 0; j < a.k; j++)
-        if (ids[threadIdx.x * a.k + j] == e) p = (int32_t) (threadIdx.x * a.k + j);
-    const uint64_t has = __ballot(p >= 0);
-    if (p >= 0) toks[__builtin_popcountll(has & ((1ull << threadIdx.x) - 1))] = p;
-    if (threadIdx.x == 0) toks[2 * kMaxTok] = __builtin_popcountll(has);
+  int32_t* toks = (int32_t*) (smem + L_.toks);  // [0, kMaxTok): the expert's picks in token order; [2 kMaxTok]: count
+  int32_t e;
+  if constexpr (NT == 1) {  // one token (NT 1 is launched for a single token alone): its pick owns the tile
+    e = a.ids[m];
+    if (threadIdx.x == 0) toks[0] = (int32_t) m, toks[2 * kMaxTok] = 1;
+  } else {
+    int32_t* ids = (int32_t*) (smem + L_.ids);
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) ids[i] = a.ids[i];
+    __syncthreads();
+    e = __builtin_amdgcn_readfirstlane(ids[m]);  // (uniform: scalar addressing)
+    // the expert's first pick owns the tile; the others leave (the same decision in every thread)
+    int dup = 0;
+    for (uint32_t j = threadIdx.x; j < m; j += kThreads) dup |= ids[j] == e;
+    if (__syncthreads_or(dup)) return;
+    if (threadIdx.x < kWave) {  // wave 0, a lane a token: its pick of this expert if any (a token's picks are
+                                // distinct experts), placed by the count of earlier tokens that picked it
+      int32_t p = -1;
+      if (threadIdx.x < a.n_tok)
+        for (uint32_t j = 0; j < a.k; j++)
+          if (ids[threadIdx.x * a.k + j] == e) p = (int32_t) (threadIdx.x * a.k + j);
+      const uint64_t has = __ballot(p >= 0);
+      if (p >= 0) toks[__builtin_popcountll(has & ((1ull << threadIdx.x) - 1))] = p;
+      if (threadIdx.x == 0) toks[2 * kMaxTok] = __builtin_popcountll(has);
+    }
   }
   __syncthreads();
-  const int cnt = toks[2 * kMaxTok];
+  const int cnt = __builtin_amdgcn_readfirstlane(toks[2 * kMaxTok]);
   int8_t* q = (int8_t*) (smem + L_.q);
   float* d = (float*) (smem + L_.d);
   // one round of loads: the tile's gate and up rows (contiguous in each tensor), the codebook, the first chunk's x
@@ -205,10 +291,10 @@ __global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
   const uint8_t* usrc = a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb;
   const uint32_t per_seg = kGuRows * rb / 16, nw = 2 * per_seg;
   const float inv_seg = 1.0f / (float) per_seg;
-  auto wsrc = [=](uint32_t j) { return j ? usrc : gsrc; };
+  auto wsrc = [=](uint32_t j) __attribute__((always_inline)) { return j ? usrc : gsrc; };
   const int live0 = cnt < NT ? cnt : NT;
-  auto xval = [&](int live, int c0) {
-    return [=](uint32_t blk, uint32_t i) {
+  auto xval = [&](int live, int c0) __attribute__((always_inline)) {
+    return [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) {
       const uint32_t r = blk / nblk, tk = (uint32_t) toks[c0 + ((int) r < live ? (int) r : live - 1)] / a.k;
       return a.x + (uint64_t) tk * a.dim + (blk % nblk) * 32 + i;
     };
@@ -233,8 +319,8 @@ __global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
   }
   __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
-  const int lane = threadIdx.x % kWave, ll = lane % L, wave = threadIdx.x / kWave;
-  constexpr int G = kWave / L, passes = (int) kGuRows / (kWaves * G);
+  float* subs = (float*) (smem + L_.subs);  // [(m NT + t) 16 + row][s]
+  float* gv = (float*) (smem + L_.gv);      // [(m NT + t) 16 + row]
   for (int c0 = 0; c0 < cnt; c0 += NT) {
     const int live = cnt - c0 < NT ? cnt - c0 : NT;
     if (c0) {  // the next chunk's x (the previous chunk's read first)
@@ -246,77 +332,106 @@ __global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
       }
       __syncthreads();
     }
-#pragma unroll
-    for (int p = 0; p < passes; p++) {
-      const uint32_t row = (uint32_t) (p * kWaves * G + wave * G + lane / L);
-      const uint8_t *rg = smem + L_.wg + row * rb, *ru = smem + L_.wu + row * rb;
-      float ag[NT], au[NT];
-#pragma unroll
-      for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.0f;
-#pragma unroll 4
-      for (uint32_t s = ll; s < nblk; s += L) {
-        Codes cg, cu;
-        const uint32_t at = (s / per) * bb;
-        codes<T>(rg + at, (int) (s % per), cg, grid);
-        codes<T>(ru + at, (int) (s % per), cu, grid);
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-          int x[8];
-          const int4* xp = (const int4*) (q + t * a.dim + s * 32);
-          const int4 x0 = xp[0], x1 = xp[1];
-          x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
-          const float xd = d[t * nblk + s];
-          ag[t] = __builtin_fmaf(xd, block_sum<T>(cg, x), ag[t]);
-          au[t] = __builtin_fmaf(xd, block_sum<T>(cu, x), au[t]);
-        }
-      }
+    // phase A: (block, matrix, row) items, the row fastest: 32 lanes of a wave share one block's x
+    const uint32_t items = 2 * kGuRows * nblk;
+    for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
+      const uint32_t row = it % kGuRows, mm = (it / kGuRows) & 1, s = it / (2 * kGuRows);
+      Codes c;
+      codes<T>(smem + (mm ? L_.wu : L_.wg) + row * rb + (s / per) * bb, (int) (s % per), c, grid);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const float vg = tree<L>(ag[t]), vu = tree<L>(au[t]);
-        if (ll == 0 && t < live) {
-          const int pk = toks[c0 + t];
-          a.h[(uint64_t) pk * a.ff + r0 + row] = lane_swiglu(vg, vu, a.lim, a.w[pk]);
-        }
+        int x[8];
+        const int4* xp = (const int4*) (q + t * a.dim + s * 32);
+        const int4 x0 = xp[0], x1 = xp[1];
+        x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
+        subs[((mm * NT + t) * kGuRows + row) * nblk + s] = block_sum<T>(c, x);
+      }
+    }
+    __syncthreads();
+    // phase B: a chain a (matrix, token, row, logical lane), whole waves so a tree's lanes are all present
+    const uint32_t chains = 2 * NT * kGuRows * L, lgL = L == 32 ? 5 : 4;
+    for (uint32_t ch = threadIdx.x; ch < (chains + kWave - 1) / kWave * kWave; ch += kThreads) {
+      const uint32_t ll = ch & (L - 1), unit = (ch >> lgL) < 2 * NT * kGuRows ? ch >> lgL : 0, t = (unit / kGuRows) % NT;
+      const float* sb = subs + unit * nblk;
+      float acc = 0.0f;
+      for (uint32_t s = ll; s < nblk; s += L) acc = __builtin_fmaf(d[t * nblk + s], sb[s], acc);
+      const float v = tree_rt(acc, L);
+      if (ll == 0 && ch < chains) gv[unit] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < NT * kGuRows) {
+      const int t = (int) threadIdx.x / (int) kGuRows, row = (int) threadIdx.x % (int) kGuRows;
+      if (t < live) {
+        const int pk = toks[c0 + t];
+        store_coherent(a.h + (uint64_t) pk * a.ff + r0 + row,
+                       lane_swiglu(gv[t * kGuRows + row], gv[(NT + t) * kGuRows + row], a.lim, a.w[pk]));
+      }
+    }
+  }
+  if (done) {  // the tile's h rows complete (each writer's own stores), then each covered pick's count raised; the
+               // last of a pick's tiles raises its token's count, and the last of a token's picks sets its flags
+    if (threadIdx.x < NT * kGuRows) wait_stores();
+    __syncthreads();
+    if (threadIdx.x < (uint32_t) cnt) {
+      const uint32_t pk = (uint32_t) toks[threadIdx.x], n = a.n_tok * a.k, tok = pk / a.k;
+      if (__hip_atomic_fetch_add(done + pk * kCtrlStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              a.ff / kGuRows - 1 &&
+          __hip_atomic_fetch_add(done + (n + tok) * kCtrlStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              a.k - 1) {
+        uint32_t* flag = done + (n + a.n_tok + tok * kFlagCopies) * kCtrlStride;
+        for (uint32_t c = 0; c < kFlagCopies; c++)
+          __hip_atomic_store(flag + c * kCtrlStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
 }
 
-template <uint32_t T, int L>
-__global__ __launch_bounds__(kThreads) void dn_kernel(DnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+// one down tile: token t, rows tile * 8 .. + 8; with `done` (the single launch's control lines), the token's ready
+// flag waited for after the weights' loads are issued
+template <uint32_t T>
+__device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, const uint32_t* done,
+                               uint32_t* error, int L) {
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
-  const uint32_t t = blockIdx.y, r0 = blockIdx.x * kDnRows, K = a.k;
+  const uint32_t r0 = tile * kDnRows, K = a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.ff), nblk = a.ff / 32;
   const DnLds L_ = dn_lds(rb, a.ff, K, grid_bytes<T>());
-  int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: the token's pick at sorted place j; [kMaxK + j]: its expert
-  if (threadIdx.x < kWave) {  // wave 0, a lane a pick: its place in ascending expert id (then pick) by its rank
-    const uint32_t j = threadIdx.x;
-    const int32_t ex = j < K ? a.ids[t * K + j] : INT32_MAX;
-    uint32_t rank = 0;
-    for (uint32_t i = 0; i < K; i++) {
-      const int32_t o = __shfl(ex, (int) i, kWave);
-      rank += o < ex || (o == ex && i < j);
-    }
-    if (j < K) picks[rank] = (int32_t) (t * K + j), picks[kMaxK + rank] = ex;
-  }
+  int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: pick j's expert; [kMaxK + r]: the pick j of rank r
+  if (threadIdx.x < K) picks[threadIdx.x] = a.ids[t * K + threadIdx.x];
   __syncthreads();
   int8_t* q = (int8_t*) (smem + L_.q);
   float* d = (float*) (smem + L_.d);
-  // one round of loads: the k experts' tile rows, the codebook, the k picks' activations
+  // one round of loads: the k experts' tile rows (in pick order), the codebook; then (their h ready) the activations
   const uint8_t* down = a.down + (uint64_t) r0 * rb;
   const uint64_t db = a.down_bytes;
   const uint32_t per_seg = kDnRows * rb / 16, nw = K * per_seg;
   const float inv_seg = 1.0f / (float) per_seg;
-  auto wsrc = [=](uint32_t j) { return down + (uint64_t) picks[kMaxK + j] * db; };
-  auto hval = [=](uint32_t blk, uint32_t i) { return a.h + (uint64_t) picks[blk / nblk] * a.ff + (blk % nblk) * 32 + i; };
+  auto wsrc = [=](uint32_t j) __attribute__((always_inline)) { return down + (uint64_t) picks[j] * db; };
+  auto hval = [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) { return a.h + (uint64_t) (t * K + blk / nblk) * a.ff + (blk % nblk) * 32 + i; };
   const uint32_t hblocks = K * nblk;
   {
     Staged st;
     Rounded rh;
     stage_load(st, wsrc, nw, per_seg, inv_seg, 0);
-    round_load(rh, hval, hblocks, 0);
     grid_copy<T>(smem + L_.grid);
+    if (threadIdx.x < kWave) {  // wave 0, a lane a pick: its rank in ascending expert id (then pick); and its h
+      const uint32_t j = threadIdx.x;
+      const int32_t ex = j < K ? picks[j] : INT32_MAX;
+      uint32_t rank = 0;
+      for (uint32_t i = 0; i < K; i++) {
+        const int32_t o = __shfl(ex, (int) i, kWave);
+        rank += o < ex || (o == ex && i < j);
+      }
+      if (j < K) picks[kMaxK + rank] = (int32_t) j;
+      if (done && j == 0) {  // the token's ready flag (bounded: a fault sets the error and goes on)
+        const uint32_t* c = done + (a.n_tok * K + a.n_tok + t * kFlagCopies + tile % kFlagCopies) * kCtrlStride;
+        uint32_t spins = __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? kSpinMax : 0;
+        while (spins < kSpinMax && !__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          spins++, __builtin_amdgcn_s_sleep(2);
+        if (spins >= kSpinMax) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (done) __syncthreads();  // the flag seen before any thread reads h
+    round_load<true>(rh, hval, hblocks, 0);
     stage_store(st, smem + L_.w, nw, 0);
     round_store(rh, hblocks, 0, nblk, a.ff, q, d);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {
@@ -324,38 +439,86 @@ __global__ __launch_bounds__(kThreads) void dn_kernel(DnArgs a) {
       stage_store(st, smem + L_.w, nw, base);
     }
     for (uint32_t base = kRoundBlocks; base < hblocks; base += kRoundBlocks) {
-      round_load(rh, hval, hblocks, base);
+      round_load<true>(rh, hval, hblocks, base);
       round_store(rh, hblocks, base, nblk, a.ff, q, d);
     }
   }
   __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
-  float* ye = (float*) (smem + L_.ye);
-  const int lane = threadIdx.x % kWave, ll = lane % L, wave = threadIdx.x / kWave;
-  constexpr int G = kWave / L, groups = (int) kDnRows / G;  // row groups a tile: a wave's G rows each
-  for (uint32_t u = wave; u < K * groups; u += kWaves) {
-    const uint32_t j = u / groups, row = (u % groups) * G + lane / L;
-    const uint8_t* wr = smem + L_.w + (j * kDnRows + row) * rb;
-    float acc = 0.0f;
-#pragma unroll 4
-    for (uint32_t s = ll; s < nblk; s += L) {
-      Codes c;
-      codes<T>(wr + (s / per) * bb, (int) (s % per), c, grid);
-      int x[8];
-      const int4* xp = (const int4*) (q + j * a.ff + s * 32);
-      const int4 x0 = xp[0], x1 = xp[1];
-      x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
-      acc = __builtin_fmaf(d[j * nblk + s], block_sum<T>(c, x), acc);
-    }
-    const float v = tree<L>(acc);
-    if (ll == 0) ye[j * kDnRows + row] = v;
+  float* subs = (float*) (smem + L_.subs);  // [j 8 + row][s]
+  float* ye = (float*) (smem + L_.ye);      // [j 8 + row]
+  // phase A: (pick, block, row) items, the row fastest: 8 lanes share one pick's block of x
+  const uint32_t items = K * kDnRows * nblk;
+  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
+    const uint32_t row = it % kDnRows, js = it / kDnRows, j = js / nblk, s = js % nblk;
+    Codes c;
+    codes<T>(smem + L_.w + (j * kDnRows + row) * rb + (s / per) * bb, (int) (s % per), c, grid);
+    int x[8];
+    const int4* xp = (const int4*) (q + j * a.ff + s * 32);
+    const int4 x0 = xp[0], x1 = xp[1];
+    x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
+    subs[(j * kDnRows + row) * nblk + s] = block_sum<T>(c, x);
   }
   __syncthreads();
-  if (threadIdx.x < kDnRows) {
+  // phase B: a chain a (pick, row, logical lane)
+  const uint32_t chains = K * kDnRows * L, lgL = L == 32 ? 5 : 4;
+  for (uint32_t ch = threadIdx.x; ch < (chains + kWave - 1) / kWave * kWave; ch += kThreads) {
+    const uint32_t ll = ch & (L - 1), unit = (ch >> lgL) < K * kDnRows ? ch >> lgL : 0, j = unit / kDnRows;
+    const float* sb = subs + unit * nblk;
+    float acc = 0.0f;
+    for (uint32_t s = ll; s < nblk; s += L) acc = __builtin_fmaf(d[j * nblk + s], sb[s], acc);
+    const float v = tree_rt(acc, L);
+    if (ll == 0 && ch < chains) ye[unit] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < kDnRows) {  // each row's k sums in ascending expert id, then add's
     float s = 0.0f;
-    for (uint32_t j = 0; j < K; j++) s = __fadd_rn(s, ye[j * kDnRows + threadIdx.x]);
+    for (uint32_t r = 0; r < K; r++) s = __fadd_rn(s, ye[picks[kMaxK + r] * kDnRows + threadIdx.x]);
     const uint64_t o = (uint64_t) t * a.dim + r0 + threadIdx.x;
     a.out[o] = __fadd_rn(s, a.add[o]);
+  }
+}
+
+template <uint32_t T, int NT, int L>
+__global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, nullptr, L);
+}
+
+template <uint32_t T, int L>
+__global__ __launch_bounds__(kThreads) void dn_kernel(DnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  dn_item<T>(a, blockIdx.y, blockIdx.x, smem, nullptr, nullptr, L);
+}
+
+// the whole layer in one launch of a workgroup a tile, gate/up tiles (pick, tile) first in block order, then down
+// tiles (token, tile). a down tile loads its weights, then waits for its picks' gate/up tiles, which wait for nothing.
+// the host launches this only when the down tiles cannot fill the chip (fewer than half its resident workgroups), so
+// whatever order the workgroups are dispatched in, a slot is always left for a gate/up tile: no deadlock. the last
+// workgroup out zeroes the control words for the next launch. gate/up and down share one quant type T here; lg / ld
+// are the contract's lane counts over dim and ff
+template <uint32_t T, int NT>
+__global__ __launch_bounds__(kThreads, 8) void layer_kernel(GuArgs ga, DnArgs da, Ctrl* ctrl, int lg, int ld) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t last;
+  const uint32_t n = ga.n_tok * ga.k, gu_tiles = ga.ff / kGuRows, dn_tiles = da.dim / kDnRows, n_gu = n * gu_tiles;
+  const uint32_t t = blockIdx.x;
+  if (t < n_gu) gu_item<T, NT>(ga, t / gu_tiles, t % gu_tiles, smem, done_of(ctrl), lg);
+  else dn_item<T>(da, (t - n_gu) / dn_tiles, (t - n_gu) % dn_tiles, smem, done_of(ctrl), &ctrl->error, ld);
+  __syncthreads();  // (every read of the control words done: their values used)
+  if (threadIdx.x == 0) {
+    const uint32_t g = t % kExitGroups, in_g = (gridDim.x - g + kExitGroups - 1) / kExitGroups;
+    const uint32_t groups = gridDim.x < kExitGroups ? gridDim.x : kExitGroups;
+    last = __hip_atomic_fetch_add(&ctrl->exited[g][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_g - 1 &&
+           __hip_atomic_fetch_add(&ctrl->top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1;
+  }
+  __syncthreads();
+  if (last) {  // every other workgroup has left
+    for (uint32_t i = threadIdx.x; i < ctrl_lines(n, ga.n_tok); i += kThreads)
+      __hip_atomic_store(done_of(ctrl) + i * kCtrlStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < kExitGroups)
+      __hip_atomic_store(&ctrl->exited[threadIdx.x][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(&ctrl->top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -10,6 +10,27 @@ namespace lane {
 
 static __constant__ Grids kGrids = make_grids();
 
+// IQ3_XXS's codebook with its signs applied: entry 16 g + s is grid entry g's 4 values (bytes 4..62), value i negated
+// where bit i of s is set, as 4 int8 in a word - a block's 8 words are then 8 lookups, no per-value sign arithmetic
+struct alignas(16) SignedIq3 {
+  uint32_t v[256 * 16];
+};
+constexpr SignedIq3 make_signed_iq3() {
+  const Grids g = make_grids();
+  SignedIq3 t{};
+  for (int e = 0; e < 256; e++)
+    for (int sg = 0; sg < 16; sg++) {
+      uint32_t w = 0;
+      for (int i = 0; i < 4; i++) {
+        const int v = (int) ((g.iq3xxs[e] >> (8 * i)) & 0xFF);
+        w |= (uint32_t) (uint8_t) (int8_t) ((sg >> i) & 1 ? -v : v) << (8 * i);
+      }
+      t.v[16 * e + sg] = w;
+    }
+  return t;
+}
+static __constant__ SignedIq3 kSignedIq3 = make_signed_iq3();
+
 // a 32-value block's int8 codes: 8 words (4 values each, value 4i + b in byte b of word i); per 8-value chunk k the
 // IQ1 types' delta (+-1, codes 8 grid + delta) or 0; per 16-value half its scale integer s21 (Q2_K, Q4_K: 8 sc) and
 // minimum m8 (8 m); the block scale d and minimum scale dmin. `bias`: a constant subtracted from every code (Q4_0's
@@ -55,14 +76,14 @@ template <> struct GridOf<kIQ2_XS> { using E = uint64_t; static constexpr int n 
 template <> struct GridOf<kIQ2_S> { using E = uint64_t; static constexpr int n = 1024; };
 template <> struct GridOf<kIQ1_S> { using E = uint64_t; static constexpr int n = 2048; };
 template <> struct GridOf<kIQ1_M> { using E = uint64_t; static constexpr int n = 2048; };
-template <> struct GridOf<kIQ3_XXS> { using E = uint32_t; static constexpr int n = 256; };
+template <> struct GridOf<kIQ3_XXS> { using E = uint32_t; static constexpr int n = 256 * 16; };  // signed
 
 template <uint32_t T> __device__ inline const typename GridOf<T>::E* const_grid() {
   if constexpr (T == kIQ2_XXS) return kGrids.iq2xxs;
   else if constexpr (T == kIQ2_XS) return kGrids.iq2xs;
   else if constexpr (T == kIQ2_S) return kGrids.iq2s;
   else if constexpr (T == kIQ1_S || T == kIQ1_M) return kGrids.iq1s;
-  else if constexpr (T == kIQ3_XXS) return kGrids.iq3xxs;
+  else if constexpr (T == kIQ3_XXS) return kSignedIq3.v;
   else return nullptr;
 }
 
@@ -123,14 +144,24 @@ template <> __device__ inline void codes<kIQ2_S>(const uint8_t* b, int j, Codes&
   c.d = f16(ld16(b));
 }
 
-// reference kernels/q8.h:97-108
+// reference kernels/q8.h:97-108 (the same codes: grid entries q[2k] and q[2k + 1] signed by ksign's 8 bits - its low
+// nibble the first entry's, its top 3 bits and the 7-bit index's parity the second's), read from the signed table;
+// the four 7-bit fields' parities at once: y folds x over 8 bits, so bit 7k of y ^ (x >> 7) is field k's parity
 template <> __device__ inline void codes<kIQ3_XXS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ3_XXS>::E* grid) {
   const uint8_t* q = b + 2 + 8 * j;
+  const uint32_t q03 = ld16(q) | ld16(q + 2) << 16, q47 = ld16(q + 4) | ld16(q + 6) << 16;
   const uint32_t aux = ld32(b + 66 + 4 * j);
+  const uint32_t x = aux & 0x0FFFFFFFu;
+  uint32_t y = x ^ (x >> 1);
+  y ^= y >> 2;
+  y ^= y >> 4;
+  const uint32_t par = y ^ (x >> 7);
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint64_t g = (uint64_t) grid[q[2 * k]] | (uint64_t) grid[q[2 * k + 1]] << 32;
-    signed8(g, ksign((aux >> (7 * k)) & 0x7F), c.w[2 * k], c.w[2 * k + 1]);
+    const uint32_t sg = (aux >> (7 * k)) & 0x7F, qq = k < 2 ? q03 : q47;
+    const uint32_t g0 = (qq >> (16 * (k % 2))) & 0xFF, g1 = (qq >> (16 * (k % 2) + 8)) & 0xFF;
+    c.w[2 * k] = (int) grid[16 * g0 + (sg & 15)];
+    c.w[2 * k + 1] = (int) grid[16 * g1 + ((sg >> 4) | ((par >> (7 * k)) & 1) << 3)];
   }
   c.s21[0] = c.s21[1] = 2 * (2 * (int) (aux >> 28) + 1);
   c.d = f16(ld16(b));

@@ -1,5 +1,5 @@
 """A routed MoE layer over the lane's int8 contract, for Python callers: the experts' three tensors resident on the
-device, one call of the C ABI's osmos_lane_layer a step (include/osmos_mi355x.h). The workspace is allocated once per
+device, one call of the C ABI's osmos_lane_layer a step (include/osmos_mi355x.h). The workspace is allocated (zeroed) once per
 token count and reused; nothing here computes - every step is the library's kernels on the given stream.
 """
 import ctypes
@@ -22,7 +22,7 @@ class LaneLayer:
     def workspace(self, n_tok):
         if n_tok not in self._ws:
             nbytes = capi.lib().osmos_lane_workspace(ctypes.byref(self.desc), n_tok)
-            ws = self.torch.empty(nbytes + 256, dtype=self.torch.uint8, device="cuda")
+            ws = self.torch.zeros(nbytes + 256, dtype=self.torch.uint8, device="cuda")
             off = (-ws.data_ptr()) % 256
             self._ws[n_tok] = (ws, ws.data_ptr() + off, nbytes)
         return self._ws[n_tok]

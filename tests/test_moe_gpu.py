@@ -160,7 +160,7 @@ def test_moe_sum_and_ops(g):
     assert (g.bits(g.host(h)) == g.bits(want)).all()
 
 
-def _lane_layer_oracle(type_, x, ids, wts, gate, up, down, dim, ff, lim):
+def _lane_layer_oracle(type_, x, ids, wts, gate, up, down, dim, ff, lim, type_down=None):
     """the reference CPU lane's layer (oracle): pairs sorted by (expert, pick), tokens' rows in ascending expert id"""
     n_tok, k = ids.shape
     pairs = sorted((int(ids[t, j]), t * k + j) for t in range(n_tok) for j in range(k))
@@ -172,7 +172,7 @@ def _lane_layer_oracle(type_, x, ids, wts, gate, up, down, dim, ff, lim):
     P = ctypes.c_void_p
     tab = lambda mats: (P * len(experts))(*[mats[e].ctypes.data for e in experts])  # noqa: E731
     ye = np.zeros((len(pairs), dim), np.float32)
-    assert orc.orc().orc_lane_layer(type_, type_, dim, ff, lim, orc.ptr(rows_x), orc.ptr(scale), len(pairs), tab(gate),
+    assert orc.orc().orc_lane_layer(type_, type_ if type_down is None else type_down, dim, ff, lim, orc.ptr(rows_x), orc.ptr(scale), len(pairs), tab(gate),
                                     tab(up), tab(down), orc.ptr(row0), orc.ptr(cnt), len(experts), orc.ptr(ye))
     row_of = {m: r for r, (_, m) in enumerate(pairs)}
     order = np.array([sorted(row_of[t * k + j] for j in range(k)) for t in range(n_tok)], np.int32).reshape(-1)
@@ -248,3 +248,80 @@ def test_lane_layer_deepseek_shape(g, name, n_tok):
     print("deepseek layer", name, n_tok, flush=True)
     L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
     assert (g.bits(g.host(out)) == g.bits(want)).all()
+
+
+def _layer_case(tg, td, n_exp, k, dim, ff, seed):
+    gate = [synth.iq_blocks(tg, ff, dim, seed + 1000 + e) for e in range(n_exp)]
+    up = [synth.iq_blocks(tg, ff, dim, seed + 2000 + e) for e in range(n_exp)]
+    down = [synth.iq_blocks(td, dim, ff, seed + 3000 + e) for e in range(n_exp)]
+    return gate, up, down
+
+
+def _route(rng, n_tok, n_exp, k):
+    ids = np.stack([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    return ids, rng.uniform(0.01, 0.3, (n_tok, k)).astype(np.float32)
+
+
+def test_lane_layer_mixed_types(g):
+    """gate/up and down of different types (the two-launch path): the oracle's bits, with a finite clamp"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    tg, td = synth.ID["IQ2_XXS"], synth.ID["IQ3_XXS"]
+    n_exp, k, dim, ff, n_tok = 16, 4, 2048, 512, 5
+    gate, up, down = _layer_case(tg, td, n_exp, k, dim, ff, 7)
+    rng = np.random.default_rng(7)
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids, wts = _route(rng, n_tok, n_exp, k)
+    want = _lane_layer_oracle(tg, x, ids, wts, gate, up, down, dim, ff, 0.75, type_down=td)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(tg, td, dim, ff, n_exp, k, D(gate), D(up), D(down), lim=0.75)
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("mixed layer", flush=True)
+    L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
+
+
+def test_lane_layer_repeat_and_graph(g):
+    """the one-launch layer's control words are left zeroed by every call: calls in a row on one workspace, and a
+    captured graph replayed with eager calls between, each the oracle's bits (shared experts across tokens too)"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t3 = synth.ID["IQ3_XXS"]
+    n_exp, k, dim, ff, n_tok = 12, 6, 1024, 256, 8
+    gate, up, down = _layer_case(t3, t3, n_exp, k, dim, ff, 11)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(t3, t3, dim, ff, n_exp, k, D(gate), D(up), D(down), lim=2.0)
+    rng = np.random.default_rng(11)
+    cases = []
+    for _ in range(3):
+        x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+        ids, wts = _route(rng, n_tok, n_exp, k)
+        add = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+        want = _lane_layer_oracle(t3, x, ids, wts, gate, up, down, dim, ff, 2.0) + add
+        cases.append(([g.dev(a) for a in (x, ids, wts, add)], want))
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("repeat layer", flush=True)
+    for _ in range(2):
+        for (x, ids, wts, add), want in cases:
+            out.fill_(float("nan"))
+            L.forward(x, ids, wts, add, out)
+            assert (g.bits(g.host(out)) == g.bits(want)).all()
+    # a graph of the first case, replayed between eager calls of the others
+    (x, ids, wts, add), want = cases[0]
+    L.workspace(n_tok)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            L.forward(x, ids, wts, add, out, stream=ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.synchronize()
+    for r in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert (g.bits(g.host(out)) == g.bits(want)).all(), r
+        (x1, ids1, wts1, add1), want1 = cases[1 + r % 2]
+        o1 = torch.full((n_tok, dim), float("nan"), device="cuda")
+        L.forward(x1, ids1, wts1, add1, o1)
+        assert (g.bits(g.host(o1)) == g.bits(want1)).all()
