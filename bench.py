@@ -8,8 +8,9 @@ step, in GB/s; weights resident in HBM and rotated through more than 2 GiB of la
 cannot serve them; steps captured in a HIP graph (the decode's launch pattern), timed with events between
 synchronizations.
 
-roofline: the dominant kernel (the fused gate/up launch of that layer) timed alone, its algorithmic bytes a launch over
-its average duration (events on the launching stream), against MI355X's 8 TB/s.
+roofline: the dominant kernel (the layer's fused gate/up launch, through osmos_lane_gate_up) timed alone, its
+algorithmic bytes a launch over its average duration (events on the launching stream), against MI355X's 8 TB/s; the
+down launch's figures beside it.
 cpu_baseline: the reference's own CPU path (oracle/_ref: src/cpu/q8.c's cpu_q8_rows and kernels/lane.h) on the host's
 cores for the same layer, rows split evenly over the threads as src/cpu/lane.c splits them.
 
@@ -116,57 +117,50 @@ def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=
                 dims=(dim, ff, n_exp, k), per_expert=per_expert)
 
 
-def gate_up_kernel_bench(torch, capi, lay, reps=20):
-    """the dominant kernel alone: q8_gate_up over the layer's step tables (built beforehand), back to back in a graph;
-    average duration a launch from events on its stream"""
+def half_bench(torch, capi, lay, half, reps=20):
+    """one fused kernel of the layer alone: osmos_lane_gate_up (fused::gu_kernel) or osmos_lane_down (fused::dn_kernel)
+    over the timed steps' routing and rotated weights, G launches back to back in a graph on stream s; the average
+    duration a launch from events recorded on s; its algorithmic bytes (each distinct expert's matrices once, the
+    activations in, the outputs out)"""
     dim, ff, n_exp, k = lay["dims"]
-    layers, ids, G, n_layers = lay["layers"], lay["ids"], lay["G"], lay["n_layers"]
+    layers, ids, w, x, G, n_layers = lay["layers"], lay["ids"], lay["w"], lay["x"], lay["G"], lay["n_layers"]
     n_tok = lay["n_tok"]
-    n = n_tok * k
     L = capi.lib()
-    i32 = lambda m: torch.zeros(m, dtype=torch.int32, device="cuda")  # noqa: E731
-    tabs = []
-    xq = torch.zeros(n_tok, dim, dtype=torch.int8, device="cuda")
-    xd = torch.zeros(n_tok, dim // 32, device="cuda")
-    L.q8_round(capi.addr(lay["x"][0]), n_tok, dim, dim, capi.addr(xq), capi.addr(xd), None)
-    for st in range(G):
-        lyr = layers[st % n_layers]
-        tb = dict(tok=i32(n), pair=i32(n), cnt=i32(n), xrow=i32(n), order=i32(n),
-                  wg=torch.zeros(n, dtype=torch.int64, device="cuda"), wu=torch.zeros(n, dtype=torch.int64, device="cuda"),
-                  wd=torch.zeros(n, dtype=torch.int64, device="cuda"))
-        base = (ctypes.c_void_p * 3)(lyr.desc.gate, lyr.desc.up, lyr.desc.down)
-        nbytes = (ctypes.c_uint64 * 3)(lyr.desc.gate_bytes, lyr.desc.up_bytes, lyr.desc.down_bytes)
-        assert L.osmos_lane_tables(capi.addr(ids[st]), n_tok, k, n_exp, base, nbytes, *(capi.addr(tb[x]) for x in (
-            "tok", "pair", "cnt", "xrow", "wg", "wu", "wd", "order")), None)
-        tabs.append(tb)
-    h = torch.zeros(n, ff, device="cuda")
-    torch.cuda.synchronize()
-    max_cnt = min(n_tok, 8)
+    h = torch.randn(G, n_tok * k, ff, device="cuda")
+    add = torch.zeros(n_tok, dim, device="cuda")
+    out = torch.zeros(G, n_tok, dim, device="cuda")
     s = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
 
     def launch_all():
         for st in range(G):
-            tb = tabs[st]
-            assert L.q8_gate_up(18, capi.addr(tb["wg"]), capi.addr(tb["wu"]), capi.addr(tb["cnt"]), capi.addr(tb["xrow"]),
-                                capi.addr(tb["tok"]), capi.addr(tb["pair"]), n, max_cnt, ff, dim, capi.addr(xq),
-                                capi.addr(xd), capi.addr(lay["w"][st]), math.inf, capi.addr(h), ff, s.cuda_stream)
+            d = ctypes.byref(layers[st % n_layers].desc)
+            if half == "gate_up":
+                ok = L.osmos_lane_gate_up(d, capi.addr(x[st]), n_tok, capi.addr(ids[st]), capi.addr(w[st]),
+                                          capi.addr(h[st]), s.cuda_stream)
+            else:
+                ok = L.osmos_lane_down(d, capi.addr(h[st]), n_tok, capi.addr(ids[st]), capi.addr(add),
+                                       capi.addr(out[st]), s.cuda_stream)
+            assert ok
 
+    graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(s):
         launch_all()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=s):
             launch_all()
     torch.cuda.synchronize()
-    graph.replay()
     ev = Events(torch)
     with torch.cuda.stream(s):
+        graph.replay()
         ms = ev.time(graph.replay, reps)
-    launches = reps * G
-    us = ms * 1e3 / launches
-    distinct = [len(set(ids[st].reshape(-1).tolist())) for st in range(G)]
-    per_launch = sum(distinct) / G * (2 * ff * (dim // 256) * 98) + n_tok * (dim + dim // 32 * 4) + n * ff * 4
-    return dict(us=us, bytes=per_launch, gbs=per_launch / (us * 1e-6) / 1e9)
+    us = ms * 1e3 / (reps * G)
+    distinct = sum(len(set(ids[st].reshape(-1).tolist())) for st in range(G)) / G
+    per_mat = ff * (dim // 256) * 98
+    if half == "gate_up":
+        nbytes = distinct * 2 * per_mat + n_tok * dim * 4 + n_tok * k * 8 + n_tok * k * ff * 4
+    else:
+        nbytes = distinct * per_mat + n_tok * k * ff * 4 + n_tok * k * 4 + 2 * n_tok * dim * 4
+    return dict(us=us, bytes=nbytes, gbs=nbytes / (us * 1e-6) / 1e9)
 
 
 def cpu_baseline(lay, seconds=10.0):
@@ -245,8 +239,10 @@ def main():
     log("config 3 layer, batch 1")
     lay = moe_layer_bench(torch, capi, 1, args.steps, args.warmup)
     log("  %.2f us a step, %.1f GB/s" % (lay["ms_per_step"] * 1e3, lay["gbs"]))
-    ker = gate_up_kernel_bench(torch, capi, lay)
-    log("  gate_up kernel: %.2f us, %.1f GB/s" % (ker["us"], ker["gbs"]))
+    ker = half_bench(torch, capi, lay, "gate_up")
+    log("  gate/up kernel: %.2f us, %.1f GB/s" % (ker["us"], ker["gbs"]))
+    dn = half_bench(torch, capi, lay, "down")
+    log("  down kernel: %.2f us, %.1f GB/s" % (dn["us"], dn["gbs"]))
     line = {
         "metric": METRIC, "value": round(lay["gbs"], 2), "unit": "GB/s", "n_gpus": 1, "steps": lay["steps"],
         "warmup": args.warmup, "ms_per_step": round(lay["ms_per_step"], 6), "higher_is_better": True,
@@ -256,8 +252,11 @@ def main():
                    "pct_hbm_peak": round(100 * lay["gbs"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(ker["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ker["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "osm::lane::gate_up_kernel<IQ3_XXS,1,16>", "us_per_launch": round(ker["us"], 3),
+                     "kernel": "osm::fused::gu_kernel<IQ3_XXS,1,16>", "us_per_launch": round(ker["us"], 3),
                      "bytes_per_launch": int(ker["bytes"])},
+        "kernels": {"osm::fused::dn_kernel<IQ3_XXS,16>": {"us_per_launch": round(dn["us"], 3),
+                                                          "bytes_per_launch": int(dn["bytes"]),
+                                                          "GB/s": round(dn["gbs"], 2)}},
     }
     if not args.no_cpu:
         log("cpu baseline")

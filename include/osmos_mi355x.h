@@ -34,9 +34,8 @@ bool osmos_lane_tables(const int32_t *ids, uint32_t n_tok, uint32_t k, uint32_t 
    ascending expert id and add[t] added after (ops_gather_sum_add) into out (n_tok rows of dim). the bits of the
    reference CPU lane for every token, whatever n_tok. `gate`, `up`, `down`: each tensor's n_exp experts back to back,
    an expert `*_bytes` apart (GGUF rows: gate/up ff rows of dim, down dim rows of ff); ids / w: the router's n_tok x k
-   picks and weights. workspace: device memory of osmos_lane_workspace bytes (256-aligned), the caller's, zeroed once
-   before its first use (every call leaves its control words zeroed again); calls sharing a workspace must be ordered
-   on one stream. */
+   picks and weights. workspace: device memory of osmos_lane_workspace bytes (256-aligned), the caller's; calls sharing
+   a workspace must be ordered on one stream. */
 typedef struct OsmosLaneLayer
 {
   uint32_t type_gu, type_down; /* the lane's types (q8.h) */
@@ -49,5 +48,15 @@ typedef struct OsmosLaneLayer
 uint64_t osmos_lane_workspace(const OsmosLaneLayer *layer, uint32_t n_tok);
 bool osmos_lane_layer(const OsmosLaneLayer *layer, const float *x, uint32_t n_tok, const int32_t *ids, const float *w,
                       const float *add, float *out, void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* the layer's two halves, for callers that keep h themselves (osmos_lane_layer is the one followed by the other, h in
+   its workspace): gate_up writes h, n_tok k rows of ff floats (pick t k + j's activations, weight w folded in), from
+   x; down rounds h and writes out = each token's k expert rows summed in ascending expert id, then add. h 16-aligned.
+   These have no counterpart in the reference, whose lane runs the two halves as separate per-table launches
+   (src/run/hip_lane.c:115-222). */
+bool osmos_lane_gate_up(const OsmosLaneLayer *layer, const float *x, uint32_t n_tok, const int32_t *ids, const float *w,
+                        float *h, void *stream);
+bool osmos_lane_down(const OsmosLaneLayer *layer, const float *h, uint32_t n_tok, const int32_t *ids, const float *add,
+                     float *out, void *stream);
 
 #endif

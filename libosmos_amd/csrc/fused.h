@@ -153,15 +153,12 @@ struct Rounded {
     return const_cast<Rounded*>(this)->at<U>();
   }
 };
-__device__ inline f32x4 load_coherent4(const float* p);
-template <bool Coherent = false, typename Val>
+template <typename Val>
 __device__ __forceinline__ void round_load(Rounded& r, Val value, uint32_t blocks, uint32_t base) {
   const uint32_t g = threadIdx.x / 8, c = 4 * (threadIdx.x % 8);
   unroll<kRPer>([&](auto u) __attribute__((always_inline)) {
     const uint32_t blk = base + g + (kThreads / 8) * u.value;
-    const float* p = value(blk < blocks ? blk : 0, c);
-    if constexpr (Coherent) r.template at<u.value>() = load_coherent4(p);
-    else r.template at<u.value>() = *(const f32x4*) p;
+    r.template at<u.value>() = *(const f32x4*) value(blk < blocks ? blk : 0, c);
   });
 }
 __device__ inline uint32_t q8_byte(float v, float inv) { return (uint32_t) ((int) rintf(__fmul_rn(v, inv)) & 0xFF); }
@@ -213,46 +210,12 @@ __device__ __forceinline__ void grid_copy(uint8_t* lds) {
 // s = ll, ll + L, ... in order, and the lanes' xor tree - the same values in the same order as the reference's
 // per-lane loop, so the same bits.
 
-// the single launch's hand-off of h between workgroups (layer_kernel). h is written and read with device-coherent
-// accesses (agent-scope atomics: they write through and read past the XCDs' own L2s), so no cache-wide write-back or
-// invalidate is needed: a writer waits for its stores to complete (vmcnt 0) before its tile's counter is raised, and
-// a reader reads h only after it has seen the counter. the control words live in the caller's workspace, zeroed
-// before the first use; every launch leaves them zeroed.
-constexpr uint32_t kExitGroups = 64;  // exit counters (one single counter would serialize every workgroup's atomic)
-constexpr uint32_t kCtrlStride = 16;  // words between counters (a 64-byte line each)
-constexpr uint32_t kFlagCopies = 16;  // a token's ready flag, in as many lines (its down tiles poll one each)
-struct Ctrl {
-  uint32_t top, error, pad[kCtrlStride - 2];  // the groups that have left; a sticky error
-  uint32_t exited[kExitGroups][kCtrlStride];  // [g][0]: workgroups of group g (blockIdx % 64) that have left
-  // then, a line each: [n picks] each pick's finished gate/up tiles; [n_tok] each token's finished picks;
-  // [n_tok][kFlagCopies] each token's ready flag (all its picks' h written)
-};
-__host__ __device__ inline uint32_t* done_of(Ctrl* c) { return reinterpret_cast<uint32_t*>(c + 1); }
-__host__ __device__ inline uint64_t ctrl_lines(uint32_t n, uint32_t n_tok) { return n + n_tok + (uint64_t) n_tok * kFlagCopies; }
-constexpr uint32_t kSpinMax = 1u << 18;  // a down tile's wait for its picks, at most (then the error is set and it
-                                         // goes on: every wave reaches its end)
-
 // the lanes' tree over a run-time lane count (16 or 32; uniform across the wave)
 __device__ inline float tree_rt(float v, int L) { return L == 32 ? tree<32>(v) : tree<16>(v); }
 
-__device__ inline void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline f32x4 load_coherent4(const float* p) {
-  const uint64_t lo = __hip_atomic_load((const uint64_t*) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t hi = __hip_atomic_load((const uint64_t*) p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  f32x4 v;
-  v.x = __uint_as_float((uint32_t) lo), v.y = __uint_as_float((uint32_t) (lo >> 32));
-  v.z = __uint_as_float((uint32_t) hi), v.w = __uint_as_float((uint32_t) (hi >> 32));
-  return v;
-}
-// this wave's memory operations complete (the compiler moves no memory access across it)
-__device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// one gate/up tile: expert of pick m (its first pick's tile: others return at once), rows tile * 16 .. + 16; with
-// `done` (the single launch's control lines), the covered picks' counters are raised once its h rows are written
+// one gate/up tile: expert of pick m (its first pick's tile: others return at once), rows tile * 16 .. + 16
 template <uint32_t T, int NT>
-__device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t tile, uint8_t* smem, uint32_t* done, int L) {
+__device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t tile, uint8_t* smem, int L) {
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t r0 = tile * kGuRows, n = a.n_tok * a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
@@ -363,54 +326,40 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
       const int t = (int) threadIdx.x / (int) kGuRows, row = (int) threadIdx.x % (int) kGuRows;
       if (t < live) {
         const int pk = toks[c0 + t];
-        store_coherent(a.h + (uint64_t) pk * a.ff + r0 + row,
-                       lane_swiglu(gv[t * kGuRows + row], gv[(NT + t) * kGuRows + row], a.lim, a.w[pk]));
-      }
-    }
-  }
-  if (done) {  // the tile's h rows complete (each writer's own stores), then each covered pick's count raised; the
-               // last of a pick's tiles raises its token's count, and the last of a token's picks sets its flags
-    if (threadIdx.x < NT * kGuRows) wait_stores();
-    __syncthreads();
-    if (threadIdx.x < (uint32_t) cnt) {
-      const uint32_t pk = (uint32_t) toks[threadIdx.x], n = a.n_tok * a.k, tok = pk / a.k;
-      if (__hip_atomic_fetch_add(done + pk * kCtrlStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              a.ff / kGuRows - 1 &&
-          __hip_atomic_fetch_add(done + (n + tok) * kCtrlStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              a.k - 1) {
-        uint32_t* flag = done + (n + a.n_tok + tok * kFlagCopies) * kCtrlStride;
-        for (uint32_t c = 0; c < kFlagCopies; c++)
-          __hip_atomic_store(flag + c * kCtrlStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.h[(uint64_t) pk * a.ff + r0 + row] =
+            lane_swiglu(gv[t * kGuRows + row], gv[(NT + t) * kGuRows + row], a.lim, a.w[pk]);
       }
     }
   }
 }
 
-// one down tile: token t, rows tile * 8 .. + 8; with `done` (the single launch's control lines), the token's ready
-// flag waited for after the weights' loads are issued
+// one down tile: token t, rows tile * 8 .. + 8
 template <uint32_t T>
-__device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, const uint32_t* done,
-                               uint32_t* error, int L) {
+__device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, int L) {
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t r0 = tile * kDnRows, K = a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.ff), nblk = a.ff / 32;
   const DnLds L_ = dn_lds(rb, a.ff, K, grid_bytes<T>());
+  // one round of loads: the activations first (h is by pick, so it needs no routing), the k experts' tile rows (in
+  // pick order), the codebook
+  auto hval = [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) {
+    return a.h + (uint64_t) (t * K + blk / nblk) * a.ff + (blk % nblk) * 32 + i;
+  };
+  const uint32_t hblocks = K * nblk;
+  Rounded rh;
+  round_load(rh, hval, hblocks, 0);
   int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: pick j's expert; [kMaxK + r]: the pick j of rank r
   if (threadIdx.x < K) picks[threadIdx.x] = a.ids[t * K + threadIdx.x];
   __syncthreads();
   int8_t* q = (int8_t*) (smem + L_.q);
   float* d = (float*) (smem + L_.d);
-  // one round of loads: the k experts' tile rows (in pick order), the codebook; then (their h ready) the activations
   const uint8_t* down = a.down + (uint64_t) r0 * rb;
   const uint64_t db = a.down_bytes;
   const uint32_t per_seg = kDnRows * rb / 16, nw = K * per_seg;
   const float inv_seg = 1.0f / (float) per_seg;
   auto wsrc = [=](uint32_t j) __attribute__((always_inline)) { return down + (uint64_t) picks[j] * db; };
-  auto hval = [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) { return a.h + (uint64_t) (t * K + blk / nblk) * a.ff + (blk % nblk) * 32 + i; };
-  const uint32_t hblocks = K * nblk;
   {
     Staged st;
-    Rounded rh;
     stage_load(st, wsrc, nw, per_seg, inv_seg, 0);
     grid_copy<T>(smem + L_.grid);
     if (threadIdx.x < kWave) {  // wave 0, a lane a pick: its rank in ascending expert id (then pick); and its h
@@ -422,16 +371,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
         rank += o < ex || (o == ex && i < j);
       }
       if (j < K) picks[kMaxK + rank] = (int32_t) j;
-      if (done && j == 0) {  // the token's ready flag (bounded: a fault sets the error and goes on)
-        const uint32_t* c = done + (a.n_tok * K + a.n_tok + t * kFlagCopies + tile % kFlagCopies) * kCtrlStride;
-        uint32_t spins = __hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? kSpinMax : 0;
-        while (spins < kSpinMax && !__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-          spins++, __builtin_amdgcn_s_sleep(2);
-        if (spins >= kSpinMax) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
-    if (done) __syncthreads();  // the flag seen before any thread reads h
-    round_load<true>(rh, hval, hblocks, 0);
     stage_store(st, smem + L_.w, nw, 0);
     round_store(rh, hblocks, 0, nblk, a.ff, q, d);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {
@@ -439,7 +379,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
       stage_store(st, smem + L_.w, nw, base);
     }
     for (uint32_t base = kRoundBlocks; base < hblocks; base += kRoundBlocks) {
-      round_load<true>(rh, hval, hblocks, base);
+      round_load(rh, hval, hblocks, base);
       round_store(rh, hblocks, base, nblk, a.ff, q, d);
     }
   }
@@ -482,44 +422,13 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
 template <uint32_t T, int NT, int L>
 __global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, nullptr, L);
+  gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
 template <uint32_t T, int L>
 __global__ __launch_bounds__(kThreads) void dn_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  dn_item<T>(a, blockIdx.y, blockIdx.x, smem, nullptr, nullptr, L);
-}
-
-// the whole layer in one launch of a workgroup a tile, gate/up tiles (pick, tile) first in block order, then down
-// tiles (token, tile). a down tile loads its weights, then waits for its picks' gate/up tiles, which wait for nothing.
-// the host launches this only when the down tiles cannot fill the chip (fewer than half its resident workgroups), so
-// whatever order the workgroups are dispatched in, a slot is always left for a gate/up tile: no deadlock. the last
-// workgroup out zeroes the control words for the next launch. gate/up and down share one quant type T here; lg / ld
-// are the contract's lane counts over dim and ff
-template <uint32_t T, int NT>
-__global__ __launch_bounds__(kThreads, 8) void layer_kernel(GuArgs ga, DnArgs da, Ctrl* ctrl, int lg, int ld) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ uint32_t last;
-  const uint32_t n = ga.n_tok * ga.k, gu_tiles = ga.ff / kGuRows, dn_tiles = da.dim / kDnRows, n_gu = n * gu_tiles;
-  const uint32_t t = blockIdx.x;
-  if (t < n_gu) gu_item<T, NT>(ga, t / gu_tiles, t % gu_tiles, smem, done_of(ctrl), lg);
-  else dn_item<T>(da, (t - n_gu) / dn_tiles, (t - n_gu) % dn_tiles, smem, done_of(ctrl), &ctrl->error, ld);
-  __syncthreads();  // (every read of the control words done: their values used)
-  if (threadIdx.x == 0) {
-    const uint32_t g = t % kExitGroups, in_g = (gridDim.x - g + kExitGroups - 1) / kExitGroups;
-    const uint32_t groups = gridDim.x < kExitGroups ? gridDim.x : kExitGroups;
-    last = __hip_atomic_fetch_add(&ctrl->exited[g][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_g - 1 &&
-           __hip_atomic_fetch_add(&ctrl->top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1;
-  }
-  __syncthreads();
-  if (last) {  // every other workgroup has left
-    for (uint32_t i = threadIdx.x; i < ctrl_lines(n, ga.n_tok); i += kThreads)
-      __hip_atomic_store(done_of(ctrl) + i * kCtrlStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x < kExitGroups)
-      __hip_atomic_store(&ctrl->exited[threadIdx.x][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) __hip_atomic_store(&ctrl->top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  dn_item<T>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
 }  // namespace fused

@@ -325,3 +325,38 @@ def test_lane_layer_repeat_and_graph(g):
         o1 = torch.full((n_tok, dim), float("nan"), device="cuda")
         L.forward(x1, ids1, wts1, add1, o1)
         assert (g.bits(g.host(o1)) == g.bits(want1)).all()
+
+
+def test_lane_layer_halves(g):
+    """osmos_lane_gate_up then osmos_lane_down (h kept by the caller): the same bits as osmos_lane_layer, and as the
+    oracle"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t3 = synth.ID["IQ3_XXS"]
+    n_exp, k, dim, ff, n_tok = 12, 6, 1024, 256, 3
+    gate, up, down = _layer_case(t3, t3, n_exp, k, dim, ff, 23)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(t3, t3, dim, ff, n_exp, k, D(gate), D(up), D(down))
+    rng = np.random.default_rng(23)
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids, wts = _route(rng, n_tok, n_exp, k)
+    want = _lane_layer_oracle(t3, x, ids, wts, gate, up, down, dim, ff, math.inf)
+    xd, idd, wd, add = g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda")
+    h = torch.full((n_tok * k, ff), float("nan"), device="cuda")
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    lib = capi.lib()
+    print("layer halves", flush=True)
+    assert lib.osmos_lane_gate_up(ctypes.byref(L.desc), capi.addr(xd), n_tok, capi.addr(idd), capi.addr(wd),
+                                  capi.addr(h), None)
+    assert lib.osmos_lane_down(ctypes.byref(L.desc), capi.addr(h), n_tok, capi.addr(idd), capi.addr(add),
+                               capi.addr(out), None)
+    torch.cuda.synchronize()
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
+    one = torch.full((n_tok, dim), float("nan"), device="cuda")
+    L.forward(xd, idd, wd, add, one)
+    assert (g.bits(g.host(one)) == g.bits(want)).all()
+    # refusals: nothing queued
+    assert not lib.osmos_lane_gate_up(ctypes.byref(L.desc), capi.addr(xd), 0, capi.addr(idd), capi.addr(wd),
+                                      capi.addr(h), None)
+    assert not lib.osmos_lane_down(ctypes.byref(L.desc), capi.addr(h), 65, capi.addr(idd), capi.addr(add),
+                                   capi.addr(out), None)
