@@ -228,6 +228,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="also the other BASELINE configs, as extra lines")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain device copy of 64 MiB, 8 times (the calibration kernel of a counter run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (--gpus %d refused)" % args.gpus)
@@ -258,6 +260,16 @@ def main():
                                                           "bytes_per_launch": int(dn["bytes"]),
                                                           "GB/s": round(dn["gbs"], 2)}},
     }
+    traffic = os.path.join(ROOT, "profiles", "gu_kernel_iq3xxs_bs1_traffic.json")
+    if os.path.exists(traffic):  # HBM bytes a launch, from the counter runs that file records
+        with open(traffic) as f:
+            line["roofline"]["traffic"] = json.load(f)["hbm_bytes_per_launch"]
+    if args.copy_probe:
+        a = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(8):
+            b.copy_(a)
+        torch.cuda.synchronize()
     if not args.no_cpu:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(lay, args.cpu_seconds)
