@@ -43,6 +43,12 @@ void q4x_expert_bounds(uint32_t n, uint32_t n_exp, Q4xExpertBounds *b);
 /* replaces reference include/osmos/gpu/q4x_ops.h:155-156 (kernels/q4x_moe.hip:220-233) */
 bool q4x_expert_tiles(const int32_t *ids, uint32_t n, uint32_t k, uint32_t n_exp, uint32_t dim, uint32_t ff,
                       const Q4xExpertTiles *t, void *stream);
+/* replaces reference include/osmos/gpu/q4x_ops.h:159-160 (kernels/q4x_moe.hip:235-253): the experts' activation
+   straight into the down's f16 - slot s's column c is silu(g[r][c]) u[r][c] (silu(x) = x / (1 + exp(-x))) for its row
+   r = idx[s] (-1: zero), rounded to f16 and tiled as mm_x16_rows (mm.h) lays it, *overflow set past f16's range (the
+   slots past `slots` in the last tile untouched). ff a multiple of 16, x16 16-byte aligned, overflow not NULL */
+bool q4x_swiglu_rows(const float *g, const float *u, uint32_t ff, const int32_t *idx, uint32_t slots, void *x16,
+                     int32_t *overflow, void *stream);
 /* replaces reference include/osmos/gpu/q4x_ops.h:161-162 (kernels/q4x_moe.hip:274-285) */
 bool q4x_moe_sum(const float *y, const int32_t *where, const float *w, uint32_t n_tok, uint32_t k, uint32_t dim,
                  const float *shared, const float *shared_logit, float *out, void *stream);

@@ -34,6 +34,14 @@ SIGS = {
     "q4x_expert_bounds": (None, [U32, U32, P]),
     "q4x_expert_tiles": (B, [P, U32, U32, U32, U32, U32, P, P]),
     "q4x_moe_sum": (B, [P, P, P, U32, U32, U32, P, P, P, P]),
+    "q4x_swiglu_rows": (B, [P, P, U32, P, U32, P, P, P]),
+    "mm_known": (B, [U32]),
+    "mm_fits": (B, [U32, U32, U32]),
+    "mm_col_tiles": (U32, [U32, U32]),
+    "mm_x16": (B, [P, U32, U32, U32, P, P, P]),
+    "mm_x16_rows": (B, [P, U32, P, U32, U32, P, P, P]),
+    "mm_run": (B, [U32, P, U32, U32, P, U32, P, U32, P]),
+    "mm_group": (B, [U32, P, P, U32, U32, U32, U32, P, P, U32, P, P, U32, P]),
     "ops_swiglu_lane": (B, [P, P, U32, F32, P, U32, P, P]),
     "ops_gather_rows": (B, [P, P, P, U32, U32, P]),
     "ops_gather_sum_add": (B, [P, P, P, U32, U32, U32, P, P]),

@@ -8,6 +8,7 @@
 // sigmoid-gated shared expert), reference include/osmos/gpu/ops.h:311-355 and kernels/ops.hip:502-525 (swiglu_lane,
 // gather_rows, gather_sum_add), reference src/run/hip_lane.c:115-200 (the lane's entries and token order).
 #include "common.h"
+#include "x16.h"
 
 extern "C" {
 #include "../../include/osmos_mi355x.h"
@@ -22,6 +23,7 @@ constexpr int kTile = 16, kPart = kTile << (Q4X_TILE_RUNS - 1);  // 128: an entr
 
 __device__ inline float pick_key(float x) { return x == x ? x : -__builtin_inff(); }
 __device__ inline float sigmoid(float x) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x))); }
+__device__ inline float silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x))); }  // (kernels/block.h:87)
 
 // ---- q4x_route: a workgroup a token; the softmax by workgroup trees, the picks by its first wave ----
 constexpr int kRouteThreads = 256, kRouteLane = kMaxExperts / kWave;
@@ -284,6 +286,27 @@ __global__ __launch_bounds__(kLaneThreads) void lane_tables_kernel(const int32_t
 
 inline unsigned grid256(uint64_t n) { return (unsigned) ((n + 255) / 256); }
 
+// ---- q4x_swiglu_rows (kernels/q4x_moe.hip:235-253): a thread 8 columns of a slot, silu(g) u (swiglu_kernel's
+// expression) rounded to f16 as mm_x16_rows rounds ----
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          uint32_t ff, const int32_t* __restrict__ idx, uint32_t slots,
+                                                          _Float16* __restrict__ x16, int32_t* __restrict__ overflow) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x, groups = ff / 8;
+  const uint32_t sl = i / groups, c = (i % groups) * 8;
+  if (sl >= slots) return;
+  const int32_t r = idx[sl];
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  half8 h;
+  bool over = false;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint64_t at = (uint64_t) (r >= 0 ? r : 0) * ff + c + j;
+    h[j] = x16_round(r >= 0 ? __fmul_rn(silu(g[at]), u[at]) : 0.0f, over);
+  }
+  *(half8*) (x16 + x16_at(sl, c, ff)) = h;
+  if (over) *overflow = 1;
+}
+
 }  // namespace moe
 }  // namespace osm
 
@@ -319,6 +342,15 @@ extern "C" OSM_API bool q4x_expert_tiles(const int32_t* ids, uint32_t n, uint32_
   moe::tiles_kernel<<<1, moe::kTileThreads, 0, s>>>(ids, n, k, n_exp, dim, ff, *t, bd);
   if (hipGetLastError() != hipSuccess) return false;
   if (n > moe::kPlaceInline) moe::place_kernel<<<n_exp, moe::kPlaceThreads, 0, s>>>(ids, n, k, n_exp, *t);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool q4x_swiglu_rows(const float* g, const float* u, uint32_t ff, const int32_t* idx,
+                                        uint32_t slots, void* x16, int32_t* overflow, void* stream) {
+  if (!g || !u || !idx || !x16 || (uintptr_t) x16 % 16 || !overflow || !slots || !ff || ff % kX16Tile) return false;
+  const uint64_t threads = (uint64_t) slots * (ff / 8);
+  moe::swiglu_rows_kernel<<<(uint32_t) ((threads + 255) / 256), 256, 0, (hipStream_t) stream>>>(
+      g, u, ff, idx, slots, (_Float16*) x16, overflow);
   return hipGetLastError() == hipSuccess;
 }
 

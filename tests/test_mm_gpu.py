@@ -1,0 +1,200 @@
+"""The f16 matrix products on the MI355X through the C ABI (mm_x16, mm_x16_rows, mm_run, mm_group, mm_known, mm_fits,
+mm_col_tiles) and the experts' activation into the down's f16 (q4x_swiglu_rows).
+
+What pins them (the reference's own checks, tests/gpu/test_mm_gpu.hip:1-5,321-341): a token's outputs the same bits
+alone, among others and reordered (batch invariance); each output within (cols/16 + 20) u sum |w16 x16| of the double
+sum over the f16 weights (the oracle's exact decode, rounded to nearest f16) and the f16 activations it reads; the
+x16 layout and rounding exactly (numpy's f16 conversion is round-to-nearest-even). mm_group's tiles the bits of
+mm_run's. q4x_swiglu_rows: silu(g) u in f32 (libm exp: parity unpinned to the bit, within an f16 ulp), then f16.
+"""
+import numpy as np
+import pytest
+
+from libosmos_amd import synth
+from oracle import orc
+
+pytestmark = pytest.mark.gpu
+
+MM_TYPES = ["Q8_0", "Q4_0", "IQ4_NL", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS",
+            "IQ1_S", "IQ1_M", "IQ4_XS"]
+U = 2.0 ** -24
+
+
+@pytest.fixture(scope="module")
+def g():
+    import torch  # noqa: F401
+    from tests import gpu_util
+    return gpu_util
+
+
+def x16_layout(x, n16=None):
+    """numpy restatement of the tiled f16 layout: token t's column c at (t/16) 16 cols + (c/16) 256 + (t%16) 16 + c%16"""
+    n, cols = x.shape
+    n16 = n16 or (n + 15) // 16 * 16
+    full = np.zeros((n16, cols), np.float16)
+    full[:n] = x.astype(np.float16)
+    return full.reshape(n16 // 16, 16, cols // 16, 16).transpose(0, 2, 1, 3).reshape(-1)
+
+
+def mm_x16(g, x):
+    import torch
+    n, cols = x.shape
+    xt = g.dev(x)
+    x16 = torch.zeros((n + 15) // 16 * 16 * cols, dtype=torch.float16, device="cuda")
+    ov = torch.zeros(1, dtype=torch.int32, device="cuda")
+    g.call("mm_x16", g.a(xt), cols, n, cols, g.a(x16), g.a(ov), None)
+    return x16, int(g.host(ov)[0])
+
+
+def run(g, name, w, rows, cols, x16, n):
+    import torch
+    y = torch.full((n, rows), float("nan"), device="cuda")
+    g.call("mm_run", synth.ID[name], g.a(g.dev(w)), rows, cols, g.a(x16), n, g.a(y), rows, None)
+    return g.host(y)
+
+
+def bound_check(name, w, rows, cols, x, y):
+    wf = orc.dequant(synth.ID[name], w, rows * cols).reshape(rows, cols).astype(np.float16).astype(np.float64)
+    xf = x.astype(np.float16).astype(np.float64)
+    want = xf @ wf.T
+    mag = np.abs(xf) @ np.abs(wf).T
+    err = np.abs(y.astype(np.float64) - want)
+    assert np.isfinite(y).all()
+    assert (err <= (cols / 16 + 20) * U * mag).all(), (name, float((err / np.maximum(mag * U, 1e-300)).max()))
+
+
+def test_x16_layout_and_overflow(g):
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 3, (21, 64)).astype(np.float32)
+    x16, ov = mm_x16(g, x)
+    assert ov == 0
+    assert (g.host(x16).view(np.uint16) == x16_layout(x).view(np.uint16)).all()
+    x[3, 5] = 70000.0  # past f16's range
+    _, ov = mm_x16(g, x)
+    assert ov == 1
+    # rows: slots from rows of x, -1 zero
+    import torch
+    idx = np.array([4, -1, 0, 20, 4], np.int32)
+    xt = g.dev(x)
+    x16 = torch.full((16 * 64,), float("nan"), dtype=torch.float16, device="cuda")
+    ov = torch.zeros(1, dtype=torch.int32, device="cuda")
+    g.call("mm_x16_rows", g.a(xt), 64, g.a(g.dev(idx)), 5, 64, g.a(x16), g.a(ov), None)
+    sel = np.stack([x[i] if i >= 0 else np.zeros(64, np.float32) for i in idx])
+    assert (g.host(x16).view(np.uint16) == x16_layout(sel).view(np.uint16)).all()
+    assert int(g.host(ov)[0]) == 0
+
+
+def test_queries():
+    from libosmos_amd import capi
+    L = capi.lib()
+    for name in MM_TYPES:
+        t = synth.ID[name]
+        assert L.mm_known(t)
+        assert L.mm_fits(t, 64, 512) and not L.mm_fits(t, 60, 512) and not L.mm_fits(t, 64, 0)
+        assert L.mm_col_tiles(t, 1) == 1 and L.mm_col_tiles(t, 17) == 2 and L.mm_col_tiles(t, 512) == 4
+    assert not L.mm_known(0) and L.mm_col_tiles(0, 16) == 0
+    assert not L.mm_fits(synth.ID["Q4_K"], 64, 128)  # not whole 256-value blocks
+
+
+@pytest.mark.parametrize("name", MM_TYPES)
+def test_mm_run_bound_and_invariance(g, name):
+    rows, cols = 96, 512
+    w = synth.random_blocks(synth.ID[name], rows, cols, 7)
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, (37, cols)).astype(np.float32)
+    print("mm", name, flush=True)
+    x16, _ = mm_x16(g, x)
+    y = run(g, name, w, rows, cols, x16, 37)
+    bound_check(name, w, rows, cols, x, y)
+    # a token's bits its own: alone, and in a reordered batch
+    for t in (0, 17, 36):
+        one16, _ = mm_x16(g, x[t:t + 1])
+        assert (g.bits(run(g, name, w, rows, cols, one16, 1)[0]) == g.bits(y[t])).all()
+    perm = rng.permutation(37)
+    p16, _ = mm_x16(g, x[perm])
+    yp = run(g, name, w, rows, cols, p16, 37)
+    assert (g.bits(yp) == g.bits(y[perm])).all()
+
+
+@pytest.mark.parametrize("name", ["IQ3_XXS", "Q4_K", "IQ2_XXS"])
+def test_mm_run_wide(g, name):
+    """DeepSeek-sized columns (7168) and 80 tokens (5 tiles: two launches' worth of 4-tile blocks)"""
+    rows, cols = 64, 7168
+    w = synth.iq_blocks(synth.ID[name], rows, cols, 9) if name.startswith("IQ") else synth.random_blocks(
+        synth.ID[name], rows, cols, 9)
+    x = np.random.default_rng(5).normal(0, 1, (80, cols)).astype(np.float32)
+    x16, _ = mm_x16(g, x)
+    y = run(g, name, w, rows, cols, x16, 80)
+    bound_check(name, w, rows, cols, x, y)
+
+
+def test_mm_group(g):
+    """three experts' gathered tokens (5, 16, 23: whole tiles each) over one x16, outputs at their own offsets: each
+    the bits of mm_run on that expert alone; an expert with 0 tokens writes nothing"""
+    import torch
+    name, rows, cols = "IQ3_XXS", 64, 1024
+    t = synth.ID[name]
+    mats = [synth.iq_blocks(t, rows, cols, 20 + e) for e in range(4)]
+    cnt = np.array([5, 16, 23, 0], np.int32)
+    rng = np.random.default_rng(8)
+    xs = [rng.normal(0, 1, (max(c, 1), cols)).astype(np.float32) for c in cnt]
+    tiles = [(c + 15) // 16 for c in cnt]
+    x16 = np.concatenate([x16_layout(xs[e][:max(cnt[e], 1)], 16 * max(tiles[e], 1)) for e in range(4)])
+    xoff = np.cumsum([0] + [16 * max(tt, 1) * cols for tt in tiles])[:4].astype(np.uint32)
+    yoff = np.cumsum([0] + [int(c) * rows for c in cnt])[:4].astype(np.uint32)
+    y = torch.full((int(cnt.sum()) + 1, rows), float("nan"), device="cuda")
+    wd = [g.dev(m) for m in mats]
+    x16d = g.dev(x16.view(np.uint16)).view(torch.float16)
+    g.call("mm_group", t, g.a(g.table(wd)), g.a(g.dev(cnt)), 4, 23, rows, cols, g.a(x16d), g.a(g.dev(xoff)), cols,
+           g.a(y), g.a(g.dev(yoff)), rows, None)
+    got = g.host(y)
+    for e in range(3):
+        one16, _ = mm_x16(g, xs[e][:cnt[e]])
+        alone = run(g, name, mats[e], rows, cols, one16, int(cnt[e]))
+        assert (g.bits(got[yoff[e] // rows:yoff[e] // rows + cnt[e]]) == g.bits(alone)).all(), e
+    assert np.isnan(got[-1]).all()  # the empty expert's place untouched
+
+
+def test_refusals(g):
+    import torch
+    from libosmos_amd import capi
+    L = capi.lib()
+    x16 = torch.zeros(16 * 256, dtype=torch.float16, device="cuda")
+    y = torch.zeros(16, 64, device="cuda")
+    w = g.dev(synth.random_blocks(synth.ID["Q4_K"], 64, 256, 1))
+    assert not L.mm_run(0, capi.addr(w), 64, 256, capi.addr(x16), 1, capi.addr(y), 64, None)  # unknown type
+    assert not L.mm_run(synth.ID["Q4_K"], capi.addr(w), 60, 256, capi.addr(x16), 1, capi.addr(y), 64, None)
+    assert not L.mm_run(synth.ID["Q4_K"], capi.addr(w), 64, 256, capi.addr(x16), 0, capi.addr(y), 64, None)
+    assert not L.mm_run(synth.ID["Q4_K"], capi.addr(w), 64, 256, capi.addr(x16), 2049, capi.addr(y), 64, None)
+    xf = torch.zeros(4, 30, device="cuda")
+    assert not L.mm_x16(capi.addr(xf), 30, 4, 30, capi.addr(x16), None, None)  # cols not a multiple of 16
+
+
+def test_swiglu_rows(g):
+    import torch
+    rng = np.random.default_rng(12)
+    ff, rows_ = 64, 6
+    gg = rng.normal(0, 3, (rows_, ff)).astype(np.float32)
+    uu = rng.normal(0, 3, (rows_, ff)).astype(np.float32)
+    idx = np.array([2, -1, 5, 0, 2], np.int32)
+    x16 = torch.full((16 * ff,), float("nan"), dtype=torch.float16, device="cuda")
+    ov = torch.zeros(1, dtype=torch.int32, device="cuda")
+    g.call("q4x_swiglu_rows", g.a(g.dev(gg)), g.a(g.dev(uu)), ff, g.a(g.dev(idx)), 5, g.a(x16), g.a(ov), None)
+    got = g.host(x16).reshape(-1)
+    silu = (gg.astype(np.float64) / (1.0 + np.exp(-gg.astype(np.float64)))).astype(np.float32)
+    h = (silu * uu).astype(np.float32)
+    sel = np.stack([h[i] if i >= 0 else np.zeros(ff, np.float32) for i in idx])
+    want = x16_layout(sel)
+    # the slots written: within an f16 ulp of the f32 reference (exp's last bit is libm's), zeros exact
+    live = np.zeros((16, ff), bool)
+    live[:5] = True
+    livev = x16_layout(live.astype(np.float32)).astype(bool)
+    a16, b16 = got[livev].astype(np.float32), want[livev].astype(np.float32)
+    ulp = np.spacing(np.abs(want[livev]).astype(np.float16)).astype(np.float32)
+    assert (np.abs(a16 - b16) <= ulp).all()
+    zero = np.zeros((16, ff), np.float32)
+    zero[1] = 1.0  # slot 1 (idx -1): exact zeros
+    zv = x16_layout(zero).astype(bool)
+    assert (got[zv] == 0).all()
+    assert np.isnan(got[~livev]).all()  # the tile's rows past the slots untouched
+    assert int(g.host(ov)[0]) == 0
