@@ -30,6 +30,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+F16_PEAK_TFLOPS = 2500.0
 METRIC = "quant GEMV GB/s (% HBM peak) bs=1; expert GEMM int8 TOPS (% MFMA) bs=512"
 
 
@@ -64,6 +65,210 @@ def iq_weights(torch, gen, n_blocks, block_bytes, d_at=0, sigma=0.02):
     raw[:, d_at] = (d & 0xFF).to(torch.uint8)
     raw[:, d_at + 1] = ((d >> 8) & 0xFF).to(torch.uint8)
     return raw.reshape(-1)
+
+
+SCALE_AT = {"Q4_0": [0], "Q8_0": [0], "Q3_K": [108], "Q4_K": [0, 2], "IQ2_XXS": [0], "IQ3_XXS": [0], "IQ1_S": [0]}
+BLOCK = {"Q4_0": (32, 18), "Q3_K": (256, 110), "Q4_K": (256, 144), "IQ2_XXS": (256, 66), "IQ3_XXS": (256, 98),
+         "IQ1_S": (256, 50), "IQ1_M": (256, 56)}
+TYPE_ID = {"Q4_0": 2, "Q3_K": 11, "Q4_K": 12, "IQ2_XXS": 16, "IQ3_XXS": 18, "IQ1_S": 19, "IQ1_M": 29}
+
+
+def blocks_of(torch, gen, name, rows, cols, copies=1, sigma=0.02):
+    """copies x rows x cols of `name` on the device: uniform random bytes (codes, grid indices, signs, sub-scales),
+    each block's f16 scale(s) |N(0, sigma)| (IQ1_M's scale nibbles the same f16) - the BASELINE configs' synthetic
+    weights. returns uint8 [copies, rows * row bytes]"""
+    v, b = BLOCK[name]
+    nblk = copies * rows * (cols // v)
+    raw = torch.randint(0, 256, (nblk, b), dtype=torch.uint8, device="cuda", generator=gen)
+    d = (torch.randn(nblk, device="cuda", generator=gen).abs_() * sigma).half().view(torch.int16).to(torch.int32)
+    if name == "IQ1_M":  # the scale's 4 nibbles at the top of the 4 scale words (bytes 49, 51, 53, 55)
+        for k in range(4):
+            at = 49 + 2 * k
+            raw[:, at] = (raw[:, at] & 0x0F) | (((d >> (4 * k)) & 0x0F) << 4).to(torch.uint8)
+    else:
+        for at in SCALE_AT[name]:
+            raw[:, at] = (d & 0xFF).to(torch.uint8)
+            raw[:, at + 1] = ((d >> 8) & 0xFF).to(torch.uint8)
+    return raw.reshape(copies, -1)
+
+
+def graph_us(torch, launch, G, reps=10):
+    """launch(i) for i < G captured once in a graph on a side stream; the average microseconds a launch over `reps`
+    replays, events recorded on that stream"""
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for i in range(G):
+            assert launch(i, s.cuda_stream) is not False, "a launch was refused"
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(G):
+                launch(i, s.cuda_stream)
+    torch.cuda.synchronize()
+    ev = Events(torch)
+    with torch.cuda.stream(s):
+        graph.replay()
+        ms = ev.time(graph.replay, reps)
+    return ms * 1e3 / (reps * G)
+
+
+def gemv_extras(torch, capi):
+    """configs 1 and 2: one matrix (rotated copies, more than 2 GiB) a launch - the fp32 matvec (mv_strided), the lane's
+    int8 matvec (q8_group_tok, x rounded beforehand) and the f16 MFMA matmul (mm_run, x16 beforehand) at 8 / 64"""
+    L = capi.lib()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    out = {}
+    for name, rows, cols, batches in (("Q4_0", 8192, 2048, (1,)), ("Q4_K", 6144, 2048, (1, 8, 64)),
+                                      ("Q3_K", 6144, 2048, (1, 8, 64))):
+        v, b = BLOCK[name]
+        wbytes = rows * cols // v * b
+        copies = max(2, math.ceil(2.2e9 / wbytes))
+        W = blocks_of(torch, gen, name, rows, cols, copies)
+        t = TYPE_ID[name]
+        for n in batches:
+            x = torch.randn(n, cols, device="cuda", generator=gen)
+            y = torch.zeros(n, rows, device="cuda")
+            G = min(copies, 64)
+            us = graph_us(torch, lambda i, st: L.mv_strided(t, capi.addr(W[i]), rows, cols, capi.addr(x), cols, n,
+                                                            capi.addr(y), rows, st), G)
+            nb = wbytes + n * cols * 4 + n * rows * 4
+            out["%s_%dx%d_mv_f32_bs%d" % (name, cols, rows, n)] = {"us": round(us, 3), "GB/s": round(nb / us / 1e3, 1)}
+            if n <= 8:
+                q = torch.zeros(n, cols, dtype=torch.int8, device="cuda")
+                d = torch.zeros(n, cols // 32, device="cuda")
+                assert L.q8_round(capi.addr(x), n, cols, cols, capi.addr(q), capi.addr(d), None)
+                tabs = [torch.tensor([W[i].data_ptr()], dtype=torch.int64, device="cuda") for i in range(G)]
+                cnt = torch.tensor([n], dtype=torch.int32, device="cuda")
+                xrow = torch.zeros(1, dtype=torch.int32, device="cuda")
+                us = graph_us(torch, lambda i, st: L.q8_group_tok(t, capi.addr(tabs[i]), capi.addr(cnt),
+                                                                  capi.addr(xrow), None, 1, n, rows, cols, capi.addr(q),
+                                                                  capi.addr(d), capi.addr(y), rows, st), G)
+                nb = wbytes + n * (cols + cols // 32 * 4) + n * rows * 4
+                out["%s_%dx%d_lane_int8_bs%d" % (name, cols, rows, n)] = {"us": round(us, 3),
+                                                                         "GB/s": round(nb / us / 1e3, 1)}
+            if n >= 8:
+                x16 = torch.zeros((n + 15) // 16 * 16 * cols, dtype=torch.float16, device="cuda")
+                assert L.mm_x16(capi.addr(x), cols, n, cols, capi.addr(x16), None, None)
+                us = graph_us(torch, lambda i, st: L.mm_run(t, capi.addr(W[i]), rows, cols, capi.addr(x16), n,
+                                                            capi.addr(y), rows, st), G)
+                nb = wbytes + n * cols * 2 + n * rows * 4
+                out["%s_%dx%d_mm_f16_bs%d" % (name, cols, rows, n)] = {
+                    "us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                    "TFLOP/s": round(2 * rows * cols * n / us / 1e6, 2)}
+        del W
+        torch.cuda.empty_cache()
+    return out
+
+
+def deepseek_extras(torch, capi, steps=256):
+    """config 4: the DeepSeek-style expert layer (hidden 7168, expert ff 2048, 256 routed experts top-8 plus the shared
+    one as a ninth pick) through osmos_lane_layer, IQ1_S / IQ1_M / IQ2_XXS, batch 1 and 4"""
+    from libosmos_amd.layer import LaneLayer
+    dim, ff, n_exp, k = 7168, 2048, 257, 9
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    rng = torch.Generator(device="cpu")
+    rng.manual_seed(5)
+    out = {}
+    for name in ("IQ1_S", "IQ1_M", "IQ2_XXS"):
+        v, b = BLOCK[name]
+        per_mat = ff * dim // v * b
+        mats = [blocks_of(torch, gen, name, ff, dim, n_exp), blocks_of(torch, gen, name, ff, dim, n_exp),
+                blocks_of(torch, gen, name, dim, ff, n_exp)]
+        t = TYPE_ID[name]
+        lay = LaneLayer(t, t, dim, ff, n_exp, k, *mats)
+        for n in (1, 4):
+            G = 64
+            ids = torch.stack([torch.stack([torch.cat([torch.randperm(n_exp - 1, generator=rng)[:k - 1],
+                                                       torch.tensor([n_exp - 1])]) for _ in range(n)])
+                               for _ in range(G)]).to(torch.int32).cuda()
+            w = torch.softmax(torch.randn(G, n, k, generator=rng), dim=-1).cuda()
+            x = torch.randn(G, n, dim, generator=rng).cuda()
+            add = torch.zeros(n, dim, device="cuda")
+            y = torch.zeros(G, n, dim, device="cuda")
+            lay.workspace(n)
+            us = graph_us(torch, lambda i, st: lay.forward(x[i], ids[i], w[i], add, y[i], stream=st), G,
+                          reps=max(1, steps // G))
+            distinct = sum(len(set(ids[i].reshape(-1).tolist())) for i in range(G)) / G
+            nb = distinct * 3 * per_mat + n * dim * 8
+            out["deepseek_layer_%s_bs%d" % (name, n)] = {"us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                                                         "MB_per_step": round(nb / 1e6, 2)}
+        del lay, mats
+        torch.cuda.empty_cache()
+    return out
+
+
+def prefill_extras(torch, capi):
+    """config 5: 512 tokens routed top-8 over 256 experts with Zipf(1.1) load, each expert's tokens gathered in whole
+    tiles: Q4_K down (2048 -> 7168) on the int8 matrix cores (mmq_group, its x8 beforehand) and IQ2_XXS gate
+    (7168 -> 2048) on the f16 ones (mm_group, its x16 beforehand); TOPS / TFLOP/s and the fraction of MI355X's dense
+    peaks (int8 5.0 POPS, f16 2.5 PFLOP/s)"""
+    import numpy as np
+    L = capi.lib()
+    n_tok, n_exp, k = 512, 256, 8
+    rng = np.random.default_rng(11)
+    p = 1.0 / np.arange(1, n_exp + 1) ** 1.1
+    p /= p.sum()
+    ids = np.stack([rng.choice(n_exp, k, replace=False, p=p) for _ in range(n_tok)])
+    cnt = np.bincount(ids.reshape(-1), minlength=n_exp).astype(np.int32)
+    pairs = [[] for _ in range(n_exp)]
+    for t in range(n_tok):
+        for e in ids[t]:
+            pairs[e].append(t)
+    soff = np.zeros(n_exp, np.uint32)
+    idx = []
+    for e in range(n_exp):
+        soff[e] = len(idx)
+        idx += pairs[e] + [-1] * ((-len(pairs[e])) % 16)
+    slots = len(idx)
+    idx_d = torch.tensor(idx, dtype=torch.int32, device="cuda")
+    cnt_d = torch.tensor(cnt, device="cuda")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(12)
+    out = {"routing": {"tokens": n_tok, "experts": n_exp, "top_k": k, "zipf": 1.1, "busiest": int(cnt.max()),
+                       "active_experts": int((cnt > 0).sum()), "slots": slots}}
+    pairs_n = int(cnt.sum())
+    # Q4_K down on int8 MFMA: rows 7168, cols 2048
+    rows, cols = 7168, 2048
+    W = blocks_of(torch, gen, "Q4_K", rows, cols, n_exp)
+    wt = torch.tensor([W[e].data_ptr() for e in range(n_exp)], dtype=torch.int64, device="cuda")
+    x = torch.randn(n_tok, cols, device="cuda", generator=gen)
+    x8 = torch.zeros(slots * cols, dtype=torch.int8, device="cuda")
+    dx = torch.zeros(slots * cols // 32, device="cuda")
+    sx = torch.zeros(slots * cols // 32, device="cuda")
+    assert L.mmq_x8_rows(capi.addr(x), cols, capi.addr(idx_d), slots, cols, capi.addr(x8), capi.addr(dx),
+                         capi.addr(sx), None)
+    soff_d = torch.tensor(soff, device="cuda")
+    yoff_d = torch.tensor(soff.astype(np.int64) * rows, device="cuda").to(torch.int32)
+    y = torch.zeros(slots * rows, device="cuda")
+    us = graph_us(torch, lambda i, st: L.mmq_group(12, capi.addr(wt), capi.addr(cnt_d), n_exp, int(cnt.max()), rows,
+                                                   cols, capi.addr(x8), capi.addr(dx), capi.addr(sx),
+                                                   capi.addr(soff_d), capi.addr(y), capi.addr(yoff_d), rows, st), 4)
+    tops = 2.0 * rows * cols * pairs_n / us / 1e6
+    out["prefill_q4k_down_mmq_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
+                                        "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
+    del W, wt, x8, dx, sx, y
+    torch.cuda.empty_cache()
+    # IQ2_XXS gate on f16 MFMA: rows 2048, cols 7168
+    rows, cols = 2048, 7168
+    W = blocks_of(torch, gen, "IQ2_XXS", rows, cols, n_exp)
+    wt = torch.tensor([W[e].data_ptr() for e in range(n_exp)], dtype=torch.int64, device="cuda")
+    x = torch.randn(n_tok, cols, device="cuda", generator=gen)
+    x16 = torch.zeros(slots * cols, dtype=torch.float16, device="cuda")
+    assert L.mm_x16_rows(capi.addr(x), cols, capi.addr(idx_d), slots, cols, capi.addr(x16), None, None)
+    xoff_d = torch.tensor(soff.astype(np.int64) * cols, device="cuda").to(torch.int32)
+    yoff_d = torch.tensor(soff.astype(np.int64) * rows, device="cuda").to(torch.int32)
+    y = torch.zeros(slots * rows, device="cuda")
+    us = graph_us(torch, lambda i, st: L.mm_group(16, capi.addr(wt), capi.addr(cnt_d), n_exp, int(cnt.max()), rows,
+                                                  cols, capi.addr(x16), capi.addr(xoff_d), cols, capi.addr(y),
+                                                  capi.addr(yoff_d), rows, st), 4)
+    tf = 2.0 * rows * cols * pairs_n / us / 1e6
+    out["prefill_iq2xxs_gate_mm_f16"] = {"us": round(us, 1), "TFLOP/s": round(tf, 2),
+                                         "pct_f16_mfma_peak": round(100 * tf / F16_PEAK_TFLOPS, 3)}
+    del W, wt, x16, y
+    torch.cuda.empty_cache()
+    return out
 
 
 def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=0):
@@ -274,11 +479,21 @@ def main():
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(lay, args.cpu_seconds)
     if args.all:
+        del lay
+        torch.cuda.empty_cache()
         extra = {}
         for n_tok in (4, 32):
             lb = moe_layer_bench(torch, capi, n_tok, max(args.steps // 4, 64), 64)
             extra["qwen_moe_layer_iq3xxs_bs%d" % n_tok] = {"GB/s": round(lb["gbs"], 2),
                                                            "us_per_step": round(lb["ms_per_step"] * 1e3, 3)}
+            del lb
+            torch.cuda.empty_cache()
+        log("configs 1, 2")
+        extra.update(gemv_extras(torch, capi))
+        log("config 4")
+        extra.update(deepseek_extras(torch, capi))
+        log("config 5")
+        extra.update(prefill_extras(torch, capi))
         line["extra"] = extra
     print(json.dumps(line))
 
