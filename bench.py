@@ -431,6 +431,7 @@ def main():
     ap.add_argument("--steps", type=int, default=1280)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--all", action="store_true", help="also the other BASELINE configs, as extra lines")
+    ap.add_argument("--only", default="3,12,4,5", help="with --all: which extras (3: bs 4/32, 12: configs 1-2, 4, 5)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-probe", action="store_true",
@@ -482,18 +483,22 @@ def main():
         del lay
         torch.cuda.empty_cache()
         extra = {}
-        for n_tok in (4, 32):
+        only = set(args.only.split(","))
+        for n_tok in (4, 32) if "3" in only else ():
             lb = moe_layer_bench(torch, capi, n_tok, max(args.steps // 4, 64), 64)
             extra["qwen_moe_layer_iq3xxs_bs%d" % n_tok] = {"GB/s": round(lb["gbs"], 2),
                                                            "us_per_step": round(lb["ms_per_step"] * 1e3, 3)}
             del lb
             torch.cuda.empty_cache()
-        log("configs 1, 2")
-        extra.update(gemv_extras(torch, capi))
-        log("config 4")
-        extra.update(deepseek_extras(torch, capi))
-        log("config 5")
-        extra.update(prefill_extras(torch, capi))
+        if "12" in only:
+            log("configs 1, 2")
+            extra.update(gemv_extras(torch, capi))
+        if "4" in only:
+            log("config 4")
+            extra.update(deepseek_extras(torch, capi))
+        if "5" in only:
+            log("config 5")
+            extra.update(prefill_extras(torch, capi))
         line["extra"] = extra
     print(json.dumps(line))
 

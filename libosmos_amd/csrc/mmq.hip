@@ -9,8 +9,10 @@
 // bits, whatever the batch.
 //
 // CDNA4 mapping: one v_mfma_i32_16x16x32_i8 is exactly one group's 16 rows x 16 tokens of integer dots (K = 32 = the
-// contract's group), so the epilogue applies per MFMA with no reassociation. a workgroup is 16 rows x up to CT tiles
-// of 16 tokens; its 4 waves are the contract's 4 K partitions, their partial sums added in wave order through LDS.
+// contract's group), so the epilogue applies per MFMA with no reassociation. a wave owns 16 rows and keeps the 4 K
+// partitions' sums side by side in registers, for CT tiles of 16 tokens at a time, walking all of its expert's tiles;
+// a workgroup is 4 such waves (64 rows) of one expert, so an expert with no tokens costs one empty workgroup a row
+// block, not one a token tile.
 // A operand: lane l holds row l % 16's 8 codes 8 (l / 16) .. + 7 of the group (one 64-bit load of packed nibbles for
 // a pair of groups); B: token l % 16's 8 int8 at the same K (one 64-bit load from the slot tile); D: rows
 // 4 (l / 16) + i, token l % 16.
@@ -26,6 +28,7 @@ namespace mmq {
 constexpr int kWaves = 4;  // the contract's K partitions
 constexpr int kThreads = kWave * kWaves, kTile = 16, kGroups = 8, kBlockBytes = 144;
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (native: stays in registers)
 
 // a half-wave a group: its 32 values' max |x| and the codes' sum by the half-wave's tree (reference kernels/mmq.hip:33-52)
 __global__ __launch_bounds__(256) void x8_rows_kernel(const float* __restrict__ x, uint32_t xs,
@@ -54,110 +57,155 @@ __global__ __launch_bounds__(256) void x8_rows_kernel(const float* __restrict__ 
   }
 }
 
+// a workgroup: 64 rows (a wave 16) of matrix blockIdx.y over all of its cnt tokens, CT tiles of 16 at a time. each
+// wave keeps the 4 K partitions' sums side by side in registers (partition p the 256-blocks b with b % 4 == p, each
+// partition's groups in ascending order, then the 4 sums added in order - the contract's). a block's activations
+// for the CT tiles (x8 4 KB a tile, dx and sx 512 B a tile: contiguous in the slot layout) are staged in LDS by the
+// whole workgroup, the next block's loads in flight while this one's MFMAs run; lanes 0 .. 15 of each wave write the
+// block's per-row (d sc, dmin m) into the wave's table, which every lane reads for its 4 output rows
 template <int CT>
 __global__ __launch_bounds__(kThreads) void q4k_kernel(const uint8_t* const* __restrict__ wt,
-                                                       const int32_t* __restrict__ cnt, uint32_t cols,
+                                                       const int32_t* __restrict__ cnt, uint32_t rows, uint32_t cols,
                                                        const int8_t* __restrict__ x8, const float* __restrict__ dx,
                                                        const float* __restrict__ sx, const uint32_t* __restrict__ soff,
                                                        float* __restrict__ ya, const uint32_t* __restrict__ yoff,
                                                        uint32_t ys) {
-  __shared__ float scl[kWaves][kGroups][2][kTile];     // a block's 16 rows' (d sc, dmin m) by group, a wave's own
-  __shared__ float part[kWaves][CT][4][kWave];         // the partitions' sums, for the ordered total
-  const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m], row0 = blockIdx.x * kTile, c0 = blockIdx.z * kTile * CT;
-  if (c0 >= n) return;  // the whole workgroup: no barrier is reached by part of it
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, col = lane % kTile, quad = lane / kTile;
-  const uint32_t nb = cols / 256, groups = cols / MMQ_GROUP;
-  const uint64_t rb = (uint64_t) nb * kBlockBytes;
-  const uint8_t* w = wt[m] + (uint64_t) row0 * rb;
-  const uint32_t s0 = soff[m] + c0;  // the first slot: a multiple of 16
+  constexpr uint32_t kX8Tile = kGroups * MMQ_SLOTS * MMQ_GROUP;  // a tile's block of x8: 4 KB
+  constexpr uint32_t kDxTile = kGroups * MMQ_SLOTS;              // a tile's block of dx (or sx): 128 floats
+  constexpr int kXPer = CT * kX8Tile / 16 / kThreads;            // 16-byte words of x8 a thread stages (1, 2, 4)
+  constexpr int kDPer = (2 * CT * kDxTile + kThreads - 1) / kThreads;  // dx / sx values a thread stages
+  __shared__ __attribute__((aligned(16))) int8_t xs8[CT * kX8Tile];
+  __shared__ __attribute__((aligned(16))) float xds[2][CT * kDxTile];  // [0] dx, [1] sx
+  __shared__ float scl[kWaves][kGroups][2][kTile];  // a block's 16 rows' (d sc, dmin m) by group, a wave's own
+  const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
+  if (!n) return;  // (the whole workgroup)
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, col = lane % kTile, quad = lane / kTile;
+  const uint32_t row0 = blockIdx.x * kTile * kWaves + wave * kTile;
+  const bool live_rows = row0 < rows;  // (a wave past the rows still stages and meets the barriers)
+  const uint32_t nb = cols / 256, rb = nb * kBlockBytes, groups = cols / MMQ_GROUP;
+  const uint8_t* arow = wt[m] + (uint64_t) (live_rows ? row0 + col : 0) * rb;  // this lane's A row
   float* y = ya + yoff[m];
-  const int live_tiles = (int) ((n - c0 + kTile - 1) / kTile), tiles = live_tiles < CT ? live_tiles : CT;
-  float acc[CT][4];
+  for (uint32_t c0 = 0; c0 < n; c0 += kTile * CT) {
+    const uint32_t s0 = soff[m] + c0;  // the pass's first slot: a multiple of 16
+    const int live = (int) ((n - c0 + kTile - 1) / kTile), tiles = live < CT ? live : CT;
+    // a block's activations for the live tiles, into registers
+    u32x4 xr[kXPer];
+    float dr[kDPer];
+    auto load = [&](uint32_t b) __attribute__((always_inline)) {
 #pragma unroll
-  for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[ct][i] = 0.0f;
-  const uint8_t* arow = w + (uint64_t) col * rb;  // this lane's A row
-  for (uint32_t b = wave; b < nb; b += kWaves) {
-    const uint8_t* blk = arow + (uint64_t) b * kBlockBytes;
-    if (quad == 0) {  // lanes 0 .. 15: row col's header -> 8 groups' (d sc, dmin m)
-      const uint4 hd = *(const uint4*) blk;
-      const float d = f16(hd.x & 0xFFFF), dmin = f16(hd.x >> 16);
-      const uint32_t sw[3] = {hd.y, hd.z, hd.w};
-      auto sb = [&](int i) { return (int) ((sw[i / 4] >> (8 * (i % 4))) & 0xFF); };
-#pragma unroll
-      for (int g = 0; g < kGroups; g++) {
-        const int sc = g < 4 ? sb(g) & 0x3F : (sb(g + 4) & 0x0F) | ((sb(g - 4) >> 2) & 0x30);
-        const int mn = g < 4 ? sb(g + 4) & 0x3F : (sb(g + 4) >> 4) | ((sb(g) >> 2) & 0x30);
-        scl[wave][g][0][col] = __fmul_rn(d, (float) sc);
-        scl[wave][g][1][col] = __fmul_rn(dmin, (float) mn);
+      for (int u = 0; u < kXPer; u++) {
+        const uint32_t wd = threadIdx.x + u * kThreads, ct = wd / (kX8Tile / 16), off = wd % (kX8Tile / 16);
+        if ((int) ct < tiles)
+          xr[u] = *(const u32x4*) (x8 + mmq_x8_at(s0 + ct * kTile, b * kGroups * MMQ_GROUP, cols) + off * 16);
       }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll 1
-    for (int gp = 0; gp < kGroups / 2; gp++) {
-      // 8 bytes of this lane's row: codes 8 quad .. + 7 of groups 2 gp (low nibbles) and 2 gp + 1 (high)
-      const uint2 raw = *(const uint2*) (blk + 16 + gp * 32 + 8 * quad);
 #pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const int g = 2 * gp + e;
-        const uint32_t sh = 4u * (uint32_t) e;
-        const uint2 av = {(raw.x >> sh) & 0x0F0F0F0Fu, (raw.y >> sh) & 0x0F0F0F0Fu};
-        const long a = (long) (((uint64_t) av.y << 32) | av.x);
-        const uint32_t gg = b * kGroups + (uint32_t) g;
-        float ds[4], dm[4];
+      for (int u = 0; u < kDPer; u++) {  // dx then sx, CT tiles each
+        const uint32_t e = threadIdx.x + u * kThreads, which = e / (CT * kDxTile), f = e % (CT * kDxTile);
+        if (which < 2 && (int) (f / kDxTile) < tiles)
+          dr[u] = (which ? sx : dx)[mmq_dx_at(s0 + (f / kDxTile) * kTile, b * kGroups, groups) + f % kDxTile];
+      }
+    };
+    auto store = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) ds[i] = scl[wave][g][0][4 * quad + i], dm[i] = scl[wave][g][1][4 * quad + i];
+      for (int u = 0; u < kXPer; u++) ((u32x4*) xs8)[threadIdx.x + u * kThreads] = xr[u];
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) {
-          if (ct < tiles) {
-            const uint32_t slot = s0 + ct * kTile + col;
-            const uint2 bv = *(const uint2*) (x8 + mmq_x8_at(slot, gg * MMQ_GROUP + 8 * quad, cols));
-            const long bb = (long) (((uint64_t) bv.y << 32) | bv.x);
-            const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const uint64_t at = mmq_dx_at(slot, gg, groups);
-            const float dxt = dx[at], nsx = -sx[at];
+      for (int u = 0; u < kDPer; u++) {
+        const uint32_t e = threadIdx.x + u * kThreads, which = e / (CT * kDxTile), f = e % (CT * kDxTile);
+        if (which < 2) xds[which][f] = dr[u];
+      }
+    };
+    float acc[4][CT][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const float v = __fmul_rn(ds[i], dxt);
-              acc[ct][i] = __builtin_fmaf(v, (float) I[i], acc[ct][i]);
-              acc[ct][i] = __builtin_fmaf(dm[i], nsx, acc[ct][i]);
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[p][ct][i] = 0.0f;
+    // this lane's weights of a block: its row's codes 8 quad .. of the 4 group pairs, and (lanes 0 .. 15) its header
+    u32x4 wa, wb, hd;
+    auto wload = [&](uint32_t b) __attribute__((always_inline)) {
+      const uint8_t* blk = arow + (uint64_t) b * kBlockBytes;
+      const uint2 r0 = *(const uint2*) (blk + 16 + 8 * quad), r1 = *(const uint2*) (blk + 48 + 8 * quad);
+      const uint2 r2 = *(const uint2*) (blk + 80 + 8 * quad), r3 = *(const uint2*) (blk + 112 + 8 * quad);
+      wa = u32x4{r0.x, r0.y, r1.x, r1.y}, wb = u32x4{r2.x, r2.y, r3.x, r3.y};
+      if (quad == 0) hd = *(const u32x4*) blk;
+    };
+    load(0);
+    wload(0);
+    for (uint32_t b0 = 0; b0 < nb; b0 += 4) {
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const uint32_t b = b0 + (uint32_t) p;
+        if (b >= nb) break;  // (uniform)
+        __syncthreads();  // the previous block's activations read by every wave
+        store();
+        const uint2 raw0 = {wa.x, wa.y}, raw1 = {wa.z, wa.w}, raw2 = {wb.x, wb.y}, raw3 = {wb.z, wb.w};
+        const u32x4 hdc = hd;
+        if (b + 1 < nb) load(b + 1), wload(b + 1);  // in flight during this block's MFMAs
+        if (quad == 0) {  // lanes 0 .. 15: row col's header -> 8 groups' (d sc, dmin m)
+          const u32x4 hd = hdc;
+          const float d = f16(hd.x & 0xFFFF), dmin = f16(hd.x >> 16);
+          const uint32_t sw[3] = {hd.y, hd.z, hd.w};
+          auto sb = [&](int i) { return (int) ((sw[i / 4] >> (8 * (i % 4))) & 0xFF); };
+#pragma unroll
+          for (int g = 0; g < kGroups; g++) {
+            const int sc = g < 4 ? sb(g) & 0x3F : (sb(g + 4) & 0x0F) | ((sb(g - 4) >> 2) & 0x30);
+            const int mn = g < 4 ? sb(g + 4) & 0x3F : (sb(g + 4) >> 4) | ((sb(g) >> 2) & 0x30);
+            scl[wave][g][0][col] = __fmul_rn(d, (float) sc);
+            scl[wave][g][1][col] = __fmul_rn(dmin, (float) mn);
+          }
+        }
+        __syncthreads();  // this block's activations and tables written
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+          // this lane's 8 codes 8 quad .. + 7 of group g: nibbles (g % 2) of bytes 16 + 32 (g / 2) + 8 quad ..
+          const uint2 raw = g / 2 == 0 ? raw0 : g / 2 == 1 ? raw1 : g / 2 == 2 ? raw2 : raw3;
+          const uint32_t sh = 4u * (uint32_t) (g % 2);
+          const long a = (long) (((uint64_t) ((raw.y >> sh) & 0x0F0F0F0Fu) << 32) | ((raw.x >> sh) & 0x0F0F0F0Fu));
+          float ds[4], dm[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) ds[i] = scl[wave][g][0][4 * quad + i], dm[i] = scl[wave][g][1][4 * quad + i];
+#pragma unroll
+          for (int ct = 0; ct < CT; ct++) {
+            if (ct < tiles) {
+              const long bb = *(const long*) (xs8 + ct * kX8Tile + g * (MMQ_SLOTS * MMQ_GROUP) + col * MMQ_GROUP + 8 * quad);
+              const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb, v4i{0, 0, 0, 0}, 0, 0, 0);
+              const float dxt = xds[0][ct * kDxTile + g * MMQ_SLOTS + col];
+              const float nsx = -xds[1][ct * kDxTile + g * MMQ_SLOTS + col];
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
+                const float v = __fmul_rn(ds[i], dxt);
+                acc[p][ct][i] = __builtin_fmaf(v, (float) I[i], acc[p][ct][i]);
+                acc[p][ct][i] = __builtin_fmaf(dm[i], nsx, acc[p][ct][i]);
+              }
             }
           }
         }
       }
     }
-    __builtin_amdgcn_wave_barrier();  // the block's table read before the next block's is written
-  }
+    __syncthreads();  // the last block's activations read before the next pass stages its own
+    if (live_rows) {
 #pragma unroll
-  for (int ct = 0; ct < CT; ct++)
+      for (int ct = 0; ct < CT; ct++) {
+        const uint32_t t = c0 + ct * kTile + col;
+        if (ct < tiles && t < n)
 #pragma unroll
-    for (int i = 0; i < 4; i++) part[wave][ct][i][lane] = acc[ct][i];
-  __syncthreads();
-  if (wave) return;
-#pragma unroll
-  for (int ct = 0; ct < CT; ct++) {
-    const uint32_t t = c0 + ct * kTile + col;
-    if (ct < tiles && t < n)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        float s = part[0][ct][i][lane];
-#pragma unroll
-        for (int p = 1; p < kWaves; p++) s = __fadd_rn(s, part[p][ct][i][lane]);
-        y[(uint64_t) t * ys + row0 + 4 * quad + i] = s;
+          for (int i = 0; i < 4; i++) {
+            const float s = __fadd_rn(__fadd_rn(__fadd_rn(acc[0][ct][i], acc[1][ct][i]), acc[2][ct][i]), acc[3][ct][i]);
+            y[(uint64_t) t * ys + row0 + 4 * quad + i] = s;
+          }
       }
+    }
   }
 }
 
 template <int CT>
-bool q4k_launch(const void* const* w, const int32_t* cnt, uint32_t n_mat, uint32_t max_cnt, uint32_t rows,
-                uint32_t cols, const int8_t* x8, const float* dx, const float* sx, const uint32_t* soff, float* y,
+bool q4k_launch(const void* const* w, const int32_t* cnt, uint32_t n_mat, uint32_t rows, uint32_t cols,
+                const int8_t* x8, const float* dx, const float* sx, const uint32_t* soff, float* y,
                 const uint32_t* yoff, uint32_t ys, hipStream_t s) {
-  const uint32_t z = (max_cnt + kTile * CT - 1) / (kTile * CT);
-  q4k_kernel<CT><<<dim3(rows / kTile, n_mat, z), kThreads, 0, s>>>((const uint8_t* const*) w, cnt, cols, x8, dx, sx,
-                                                                   soff, y, yoff, ys);
+  const uint32_t per = kTile * kWaves;
+  q4k_kernel<CT><<<dim3((rows + per - 1) / per, n_mat), kThreads, 0, s>>>((const uint8_t* const*) w, cnt, rows, cols,
+                                                                           x8, dx, sx, soff, y, yoff, ys);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -185,8 +233,7 @@ extern "C" OSM_API bool mmq_group(uint32_t type, const void* const* w, const int
       rows % mmq::kTile || !cols || cols % 256 || ys < rows)
     return false;
   const hipStream_t s = (hipStream_t) stream;
-  if (max_cnt <= mmq::kTile) return mmq::q4k_launch<1>(w, cnt, n_mat, max_cnt, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
-  if (max_cnt <= 2 * mmq::kTile)
-    return mmq::q4k_launch<2>(w, cnt, n_mat, max_cnt, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
-  return mmq::q4k_launch<MMQ_MAX_TILES>(w, cnt, n_mat, max_cnt, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
+  if (max_cnt <= mmq::kTile) return mmq::q4k_launch<1>(w, cnt, n_mat, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
+  if (max_cnt <= 2 * mmq::kTile) return mmq::q4k_launch<2>(w, cnt, n_mat, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
+  return mmq::q4k_launch<MMQ_MAX_TILES>(w, cnt, n_mat, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
 }
