@@ -19,8 +19,8 @@ namespace fused {
 
 using namespace lane;
 
-constexpr int kThreads = 1024, kWaves = kThreads / 64;
-constexpr uint32_t kGuRows = 16, kDnRows = 8, kMaxTok = 64, kMaxK = 32;
+constexpr int kGuThreads = 256, kDnThreads = 1024;  // a gate/up tile's workgroup, a down tile's
+constexpr uint32_t kGuRows = 4, kDnRows = 8, kMaxTok = 64, kMaxK = 32;
 
 __host__ __device__ constexpr uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
@@ -116,19 +116,20 @@ __device__ __forceinline__ void unroll(F&& f) {
     unroll<N, U + 1>(f);
   }
 }
-template <typename Src>
+template <int NTH, typename Src>
 __device__ __forceinline__ void stage_load(Staged& st, Src src, uint32_t n, uint32_t per_seg, float inv, uint32_t base) {
   unroll<kPer>([&](auto u) __attribute__((always_inline)) {
-    const uint32_t l0 = base + u.value * kThreads + threadIdx.x, l = l0 < n ? l0 : 0;  // (past the end: word 0 again)
+    const uint32_t l0 = base + u.value * NTH + threadIdx.x, l = l0 < n ? l0 : 0;  // (past the end: word 0 again)
     uint32_t j = (uint32_t) ((float) l * inv);
     j -= j * per_seg > l;
     j += (j + 1) * per_seg <= l;
     st.template at<u.value>() = ((const u32x4*) src(j))[l - j * per_seg];
   });
 }
+template <int NTH>
 __device__ __forceinline__ void stage_store(const Staged& st, uint8_t* lds, uint32_t n, uint32_t base) {
   unroll<kPer>([&](auto u) __attribute__((always_inline)) {
-    const uint32_t l = base + u.value * kThreads + threadIdx.x;
+    const uint32_t l = base + u.value * NTH + threadIdx.x;
     if (l < n) ((u32x4*) lds)[l] = st.template at<u.value>();
   });
 }
@@ -139,7 +140,8 @@ __device__ __forceinline__ void stage_store(const Staged& st, uint8_t* lds, uint
 // (block base + threadIdx.x / 8 + 32 u), round_store() reduces and writes them; value(blk, c) is the address of block
 // blk's value c
 constexpr int kRPer = 2;
-constexpr uint32_t kRoundBlocks = (kThreads / 8) * kRPer;  // blocks a round
+template <int NTH>
+constexpr uint32_t kRoundBlocks = (NTH / 8) * kRPer;  // blocks a round
 struct Rounded {
   f32x4 v0, v1;
   template <int U>
@@ -153,20 +155,21 @@ struct Rounded {
     return const_cast<Rounded*>(this)->at<U>();
   }
 };
-template <typename Val>
+template <int NTH, typename Val>
 __device__ __forceinline__ void round_load(Rounded& r, Val value, uint32_t blocks, uint32_t base) {
   const uint32_t g = threadIdx.x / 8, c = 4 * (threadIdx.x % 8);
   unroll<kRPer>([&](auto u) __attribute__((always_inline)) {
-    const uint32_t blk = base + g + (kThreads / 8) * u.value;
+    const uint32_t blk = base + g + (NTH / 8) * u.value;
     r.template at<u.value>() = *(const f32x4*) value(blk < blocks ? blk : 0, c);
   });
 }
 __device__ inline uint32_t q8_byte(float v, float inv) { return (uint32_t) ((int) rintf(__fmul_rn(v, inv)) & 0xFF); }
+template <int NTH>
 __device__ __forceinline__ void round_store(const Rounded& r, uint32_t blocks, uint32_t base, uint32_t nb_row, uint32_t cols,
                                    int8_t* q, float* d) {
   const uint32_t g = threadIdx.x / 8, c = 4 * (threadIdx.x % 8);
   unroll<kRPer>([&](auto u) __attribute__((always_inline)) {
-    const uint32_t blk = base + g + (kThreads / 8) * u.value;
+    const uint32_t blk = base + g + (NTH / 8) * u.value;
     const f32x4 v = r.template at<u.value>();
     float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     am = fmaxf(am, xor_lane(am, 1));
@@ -184,20 +187,20 @@ __device__ __forceinline__ void round_store(const Rounded& r, uint32_t blocks, u
 
 
 // the codebook, copied by the first threads of a workgroup (1 - 16 KB of constant memory, 16-aligned)
-template <uint32_t T>
+template <uint32_t T, int NTH>
 __device__ __forceinline__ void grid_copy(uint8_t* lds) {
   if constexpr (grid_bytes<T>() > 0) {
     constexpr uint32_t n = grid_bytes<T>() / 16;
     const u32x4* src = (const u32x4*) const_grid<T>();
-    u32x4 v[(n + kThreads - 1) / kThreads];
+    u32x4 v[(n + NTH - 1) / NTH];
 #pragma unroll
-    for (uint32_t u = 0; u < (n + kThreads - 1) / kThreads; u++) {
-      const uint32_t l = u * kThreads + threadIdx.x;
+    for (uint32_t u = 0; u < (n + NTH - 1) / NTH; u++) {
+      const uint32_t l = u * NTH + threadIdx.x;
       v[u] = src[l < n ? l : 0];
     }
 #pragma unroll
-    for (uint32_t u = 0; u < (n + kThreads - 1) / kThreads; u++) {
-      const uint32_t l = u * kThreads + threadIdx.x;
+    for (uint32_t u = 0; u < (n + NTH - 1) / NTH; u++) {
+      const uint32_t l = u * NTH + threadIdx.x;
       if (l < n) ((u32x4*) lds)[l] = v[u];
     }
   }
@@ -213,9 +216,10 @@ __device__ __forceinline__ void grid_copy(uint8_t* lds) {
 // the lanes' tree over a run-time lane count (16 or 32; uniform across the wave)
 __device__ inline float tree_rt(float v, int L) { return L == 32 ? tree<32>(v) : tree<16>(v); }
 
-// one gate/up tile: expert of pick m (its first pick's tile: others return at once), rows tile * 16 .. + 16
+// one gate/up tile: expert of pick m (its first pick's tile: others return at once), rows tile * kGuRows .. + kGuRows
 template <uint32_t T, int NT>
 __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t tile, uint8_t* smem, int L) {
+  constexpr int kThreads = kGuThreads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t r0 = tile * kGuRows, n = a.n_tok * a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
@@ -266,18 +270,18 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   {
     Staged st;
     Rounded rx;
-    stage_load(st, wsrc, nw, per_seg, inv_seg, 0);
-    round_load(rx, xval(live0, 0), xblocks, 0);
-    grid_copy<T>(smem + L_.grid);
-    stage_store(st, smem + L_.wg, nw, 0);
-    round_store(rx, xblocks, 0, nblk, a.dim, q, d);
+    stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, 0);
+    round_load<kThreads>(rx, xval(live0, 0), xblocks, 0);
+    grid_copy<T, kThreads>(smem + L_.grid);
+    stage_store<kThreads>(st, smem + L_.wg, nw, 0);
+    round_store<kThreads>(rx, xblocks, 0, nblk, a.dim, q, d);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {  // (tiles past one round)
-      stage_load(st, wsrc, nw, per_seg, inv_seg, base);
-      stage_store(st, smem + L_.wg, nw, base);
+      stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, base);
+      stage_store<kThreads>(st, smem + L_.wg, nw, base);
     }
-    for (uint32_t base = kRoundBlocks; base < xblocks; base += kRoundBlocks) {
-      round_load(rx, xval(live0, 0), xblocks, base);
-      round_store(rx, xblocks, base, nblk, a.dim, q, d);
+    for (uint32_t base = kRoundBlocks<kThreads>; base < xblocks; base += kRoundBlocks<kThreads>) {
+      round_load<kThreads>(rx, xval(live0, 0), xblocks, base);
+      round_store<kThreads>(rx, xblocks, base, nblk, a.dim, q, d);
     }
   }
   __syncthreads();
@@ -289,13 +293,13 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
     if (c0) {  // the next chunk's x (the previous chunk's read first)
       __syncthreads();
       Rounded rx;
-      for (uint32_t base = 0; base < xblocks; base += kRoundBlocks) {
-        round_load(rx, xval(live, c0), xblocks, base);
-        round_store(rx, xblocks, base, nblk, a.dim, q, d);
+      for (uint32_t base = 0; base < xblocks; base += kRoundBlocks<kThreads>) {
+        round_load<kThreads>(rx, xval(live, c0), xblocks, base);
+        round_store<kThreads>(rx, xblocks, base, nblk, a.dim, q, d);
       }
       __syncthreads();
     }
-    // phase A: (block, matrix, row) items, the row fastest: 32 lanes of a wave share one block's x
+    // phase A: (block, matrix, row) items, the row fastest: the 2 kGuRows lanes of a block share its x
     const uint32_t items = 2 * kGuRows * nblk;
     for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
       const uint32_t row = it % kGuRows, mm = (it / kGuRows) & 1, s = it / (2 * kGuRows);
@@ -333,9 +337,10 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   }
 }
 
-// one down tile: token t, rows tile * 8 .. + 8
+// one down tile: token t, rows tile * kGuRows .. + kGuRows
 template <uint32_t T>
 __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, int L) {
+  constexpr int kThreads = kDnThreads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t r0 = tile * kDnRows, K = a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.ff), nblk = a.ff / 32;
@@ -347,7 +352,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   };
   const uint32_t hblocks = K * nblk;
   Rounded rh;
-  round_load(rh, hval, hblocks, 0);
+  round_load<kThreads>(rh, hval, hblocks, 0);
   int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: pick j's expert; [kMaxK + r]: the pick j of rank r
   if (threadIdx.x < K) picks[threadIdx.x] = a.ids[t * K + threadIdx.x];
   __syncthreads();
@@ -360,8 +365,8 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   auto wsrc = [=](uint32_t j) __attribute__((always_inline)) { return down + (uint64_t) picks[j] * db; };
   {
     Staged st;
-    stage_load(st, wsrc, nw, per_seg, inv_seg, 0);
-    grid_copy<T>(smem + L_.grid);
+    stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, 0);
+    grid_copy<T, kThreads>(smem + L_.grid);
     if (threadIdx.x < kWave) {  // wave 0, a lane a pick: its rank in ascending expert id (then pick); and its h
       const uint32_t j = threadIdx.x;
       const int32_t ex = j < K ? picks[j] : INT32_MAX;
@@ -372,15 +377,15 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
       }
       if (j < K) picks[kMaxK + rank] = (int32_t) j;
     }
-    stage_store(st, smem + L_.w, nw, 0);
-    round_store(rh, hblocks, 0, nblk, a.ff, q, d);
+    stage_store<kThreads>(st, smem + L_.w, nw, 0);
+    round_store<kThreads>(rh, hblocks, 0, nblk, a.ff, q, d);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {
-      stage_load(st, wsrc, nw, per_seg, inv_seg, base);
-      stage_store(st, smem + L_.w, nw, base);
+      stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, base);
+      stage_store<kThreads>(st, smem + L_.w, nw, base);
     }
-    for (uint32_t base = kRoundBlocks; base < hblocks; base += kRoundBlocks) {
-      round_load(rh, hval, hblocks, base);
-      round_store(rh, hblocks, base, nblk, a.ff, q, d);
+    for (uint32_t base = kRoundBlocks<kThreads>; base < hblocks; base += kRoundBlocks<kThreads>) {
+      round_load<kThreads>(rh, hval, hblocks, base);
+      round_store<kThreads>(rh, hblocks, base, nblk, a.ff, q, d);
     }
   }
   __syncthreads();
@@ -420,13 +425,13 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
 }
 
 template <uint32_t T, int NT, int L>
-__global__ __launch_bounds__(kThreads) void gu_kernel(GuArgs a) {
+__global__ __launch_bounds__(kGuThreads) void gu_kernel(GuArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
 template <uint32_t T, int L>
-__global__ __launch_bounds__(kThreads) void dn_kernel(DnArgs a) {
+__global__ __launch_bounds__(kDnThreads) void dn_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   dn_item<T>(a, blockIdx.y, blockIdx.x, smem, L);
 }

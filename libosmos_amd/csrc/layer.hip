@@ -23,7 +23,7 @@ bool gu_launch(const GuArgs& a, hipStream_t s) {
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
-  k<<<dim3(a.ff / fused::kGuRows, n), fused::kThreads, l.total, s>>>(a);
+  k<<<dim3(a.ff / fused::kGuRows, n), fused::kGuThreads, l.total, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -35,7 +35,7 @@ bool dn_launch(const DnArgs& a, hipStream_t s) {
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
-  k<<<dim3(a.dim / fused::kDnRows, a.n_tok), fused::kThreads, l.total, s>>>(a);
+  k<<<dim3(a.dim / fused::kDnRows, a.n_tok), fused::kDnThreads, l.total, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
