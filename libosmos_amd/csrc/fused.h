@@ -186,22 +186,33 @@ __device__ __forceinline__ void round_store(const Rounded& r, uint32_t blocks, u
 }
 
 
-// the codebook, copied by the first threads of a workgroup (1 - 16 KB of constant memory, 16-aligned)
+// the codebook (1 - 16 KB of constant memory, 16-aligned): grid_load() issues its loads into registers, grid_store()
+// writes them to the workgroup's LDS copy - apart, so the loads can be issued first and waited for last
 template <uint32_t T, int NTH>
-__device__ __forceinline__ void grid_copy(uint8_t* lds) {
-  if constexpr (grid_bytes<T>() > 0) {
-    constexpr uint32_t n = grid_bytes<T>() / 16;
+struct GridStage {
+  static constexpr uint32_t n = grid_bytes<T>() / 16, per = (n + NTH - 1) / NTH;
+  u32x4 v[per > 0 ? per : 1];
+};
+template <uint32_t T, int NTH>
+__device__ __forceinline__ void grid_load(GridStage<T, NTH>& g) {
+  constexpr uint32_t n = GridStage<T, NTH>::n;
+  if constexpr (n > 0) {
     const u32x4* src = (const u32x4*) const_grid<T>();
-    u32x4 v[(n + NTH - 1) / NTH];
 #pragma unroll
-    for (uint32_t u = 0; u < (n + NTH - 1) / NTH; u++) {
+    for (uint32_t u = 0; u < GridStage<T, NTH>::per; u++) {
       const uint32_t l = u * NTH + threadIdx.x;
-      v[u] = src[l < n ? l : 0];
+      g.v[u] = src[l < n ? l : 0];
     }
+  }
+}
+template <uint32_t T, int NTH>
+__device__ __forceinline__ void grid_store(const GridStage<T, NTH>& g, uint8_t* lds) {
+  constexpr uint32_t n = GridStage<T, NTH>::n;
+  if constexpr (n > 0) {
 #pragma unroll
-    for (uint32_t u = 0; u < (n + NTH - 1) / NTH; u++) {
+    for (uint32_t u = 0; u < GridStage<T, NTH>::per; u++) {
       const uint32_t l = u * NTH + threadIdx.x;
-      if (l < n) ((u32x4*) lds)[l] = v[u];
+      if (l < n) ((u32x4*) lds)[l] = g.v[u];
     }
   }
 }
@@ -225,6 +236,15 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
   const GuLds L_ = gu_lds(rb, a.dim, NT, grid_bytes<T>(), n);
   int32_t* toks = (int32_t*) (smem + L_.toks);  // [0, kMaxTok): the expert's picks in token order; [2 kMaxTok]: count
+  // loads that need no routing first: the codebook and, for one token, its x row (the pick's own token)
+  GridStage<T, kThreads> gs;
+  grid_load<T, kThreads>(gs);
+  Rounded rx;
+  if constexpr (NT == 1) {
+    const float* xrow = a.x + (uint64_t) (m / a.k) * a.dim;
+    round_load<kThreads>(rx, [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) { return xrow + blk * 32 + i; },
+                         NT * (a.dim / 32), 0);
+  }
   int32_t e;
   if constexpr (NT == 1) {  // one token (NT 1 is launched for a single token alone): its pick owns the tile
     e = a.ids[m];
@@ -269,12 +289,11 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   const uint32_t xblocks = NT * nblk;
   {
     Staged st;
-    Rounded rx;
     stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, 0);
-    round_load<kThreads>(rx, xval(live0, 0), xblocks, 0);
-    grid_copy<T, kThreads>(smem + L_.grid);
-    stage_store<kThreads>(st, smem + L_.wg, nw, 0);
+    if constexpr (NT > 1) round_load<kThreads>(rx, xval(live0, 0), xblocks, 0);
+    grid_store<T, kThreads>(gs, smem + L_.grid);
     round_store<kThreads>(rx, xblocks, 0, nblk, a.dim, q, d);
+    stage_store<kThreads>(st, smem + L_.wg, nw, 0);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {  // (tiles past one round)
       stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, base);
       stage_store<kThreads>(st, smem + L_.wg, nw, base);
@@ -353,6 +372,8 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   const uint32_t hblocks = K * nblk;
   Rounded rh;
   round_load<kThreads>(rh, hval, hblocks, 0);
+  GridStage<T, kThreads> gs;
+  grid_load<T, kThreads>(gs);
   int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: pick j's expert; [kMaxK + r]: the pick j of rank r
   if (threadIdx.x < K) picks[threadIdx.x] = a.ids[t * K + threadIdx.x];
   __syncthreads();
@@ -366,7 +387,6 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   {
     Staged st;
     stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, 0);
-    grid_copy<T, kThreads>(smem + L_.grid);
     if (threadIdx.x < kWave) {  // wave 0, a lane a pick: its rank in ascending expert id (then pick); and its h
       const uint32_t j = threadIdx.x;
       const int32_t ex = j < K ? picks[j] : INT32_MAX;
@@ -377,8 +397,9 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
       }
       if (j < K) picks[kMaxK + rank] = (int32_t) j;
     }
-    stage_store<kThreads>(st, smem + L_.w, nw, 0);
+    grid_store<T, kThreads>(gs, smem + L_.grid);
     round_store<kThreads>(rh, hblocks, 0, nblk, a.ff, q, d);
+    stage_store<kThreads>(st, smem + L_.w, nw, 0);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {
       stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, base);
       stage_store<kThreads>(st, smem + L_.w, nw, base);
