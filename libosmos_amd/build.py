@@ -2,7 +2,7 @@
 process, in parallel), linked into one shared library whose exports are exactly include/**/*.h's declarations.
 
 flags: -O3, -ffp-contract=off (every product and sum rounded on its own: the contracts' bits), packed-FP32 ops off
-(-Xclang -target-feature -Xclang -packed-fp32-ops), -fPIC. run: python -m libosmos_amd.build
+(-Xclang -target-feature -Xclang -packed-fp32-ops), MFMA results in VGPRs (-mllvm -amdgpu-mfma-vgpr-form=1), -fPIC. run: python -m libosmos_amd.build
 """
 import concurrent.futures as cf
 import os
@@ -17,6 +17,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-ffp-contract=off", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-mllvm", "-amdgpu-mfma-vgpr-form=1",  # MFMA results straight in VGPRs: the epilogues read them with no copy
          "-I" + os.path.join(os.path.dirname(HERE), "include")]
 
 
