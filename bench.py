@@ -202,8 +202,9 @@ def deepseek_extras(torch, capi, steps=256):
 def prefill_extras(torch, capi):
     """config 5: 512 tokens routed top-8 over 256 experts with Zipf(1.1) load, each expert's tokens gathered in whole
     tiles: Q4_K down (2048 -> 7168) on the int8 matrix cores (mmq_group, its x8 beforehand) and IQ2_XXS gate
-    (7168 -> 2048) on the f16 ones (mm_group, its x16 beforehand); TOPS / TFLOP/s and the fraction of MI355X's dense
-    peaks (int8 5.0 POPS, f16 2.5 PFLOP/s)"""
+    (7168 -> 2048) on the f16 ones (mm_group, its x16 beforehand) and on the int8 ones under the lane contract
+    (osmos_lane_group, its q8 rows beforehand); TOPS / TFLOP/s and the fraction of MI355X's dense peaks (int8
+    5.0 POPS, f16 2.5 PFLOP/s)"""
     import numpy as np
     L = capi.lib()
     n_tok, n_exp, k = 512, 256, 8
@@ -266,6 +267,21 @@ def prefill_extras(torch, capi):
     tf = 2.0 * rows * cols * pairs_n / us / 1e6
     out["prefill_iq2xxs_gate_mm_f16"] = {"us": round(us, 1), "TFLOP/s": round(tf, 2),
                                          "pct_f16_mfma_peak": round(100 * tf / F16_PEAK_TFLOPS, 3)}
+    # the same gate on the int8 matrix cores under the lane contract (the reference CPU lane's bits): each expert's
+    # tokens gathered in order, rounded (q8_round), then osmos_lane_group
+    order = [t for e in range(n_exp) for t in pairs[e]]
+    xg = x[torch.tensor(order, device="cuda")].contiguous()
+    q8 = torch.zeros(pairs_n, cols, dtype=torch.int8, device="cuda")
+    d8 = torch.zeros(pairs_n, cols // 32, device="cuda")
+    assert L.q8_round(capi.addr(xg), pairs_n, cols, cols, capi.addr(q8), capi.addr(d8), None)
+    xrow = torch.tensor(np.concatenate([[0], np.cumsum(cnt)[:-1]]).astype(np.int32), device="cuda")
+    y = torch.zeros(pairs_n, rows, device="cuda")
+    us = graph_us(torch, lambda i, st: L.osmos_lane_group(16, capi.addr(wt), capi.addr(cnt_d), capi.addr(xrow), n_exp,
+                                                          int(cnt.max()), rows, cols, capi.addr(q8), capi.addr(d8),
+                                                          capi.addr(y), rows, st), 4)
+    tops = 2.0 * rows * cols * pairs_n / us / 1e6
+    out["prefill_iq2xxs_gate_lane_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
+                                            "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
     del W, wt, x16, y
     torch.cuda.empty_cache()
     return out

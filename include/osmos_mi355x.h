@@ -49,6 +49,19 @@ uint64_t osmos_lane_workspace(const OsmosLaneLayer *layer, uint32_t n_tok);
 bool osmos_lane_layer(const OsmosLaneLayer *layer, const float *x, uint32_t n_tok, const int32_t *ids, const float *w,
                       const float *add, float *out, void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* the lane contract at prefill scale: q8_group_tok's sums (include/osmos/gpu/q8.h; reference kernels/q8.h:178-212,
+   src/cpu/q8.c:383-407) for any token count - matrix m (w[m], rows x cols of `type`) over rows xrow[m] ..
+   xrow[m] + cnt[m] - 1 of the rounded activations q / d (q8_round's layout), into the same rows of y (ys apart); the
+   same bits as q8_group_tok and the reference CPU lane for every row, whatever the count. no counterpart in the
+   reference (its lane stops at 8 tokens a matrix; its prompts take the f16 mm): for prompt batches of the lane's types
+   on the int8 matrix cores. types IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ1_S, IQ1_M; rows a multiple of 16, cols of 256;
+   max_cnt (the largest cnt) at most OSMOS_LANE_MAX_TOKENS. w, cnt, xrow on the device; false = refused, nothing
+   queued. */
+#define OSMOS_LANE_MAX_TOKENS 4096
+bool osmos_lane_group(uint32_t type, const void *const *w, const int32_t *cnt, const int32_t *xrow, uint32_t n_mat,
+                      uint32_t max_cnt, uint32_t rows, uint32_t cols, const int8_t *q, const float *d, float *y,
+                      uint32_t ys, void *stream);
+
 /* the layer's two halves, for callers that keep h themselves (osmos_lane_layer is the one followed by the other, h in
    its workspace): gate_up writes h, n_tok k rows of ff floats (pick t k + j's activations, weight w folded in), from
    x; down rounds h and writes out = each token's k expert rows summed in ascending expert id, then add. h 16-aligned.

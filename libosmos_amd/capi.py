@@ -73,6 +73,7 @@ SIGS.update({
     "osmos_lane_layer": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P, P, U64, P]),
     "osmos_lane_gate_up": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P]),
     "osmos_lane_down": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P]),
+    "osmos_lane_group": (B, [U32, P, P, P, U32, U32, U32, U32, P, P, P, U32, P]),
 })
 
 _lib = None
