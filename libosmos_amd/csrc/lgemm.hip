@@ -6,13 +6,13 @@
 // integer dot with the int8 activations, then ((d s21) / 8) isum per half, the halves added, fmaf'd with the block's
 // activation scale onto the lane's sum; then the lanes' xor tree (pairs ll, ll ^ L/2 first, then ll ^ L/4, ...).
 //
-// CDNA4 mapping: a wave owns 16 rows x CT tiles of 16 tokens. the integer half-dots are MFMAs: each 32-value block's
-// codes (lane l: row l % 16, values 8 (l / 16) .. + 7, decoded straight into its A operand - the IQ1 types' 8 grid +
-// delta folded into one int8 per value) go to two v_mfma_i32_16x16x32_i8, one with the second half's lanes zeroed,
-// one with the first's: the two halves' exact dots for 16 rows x 16 tokens. the float steps then run per output in the
-// contract's order. a logical lane's chain is one accumulator: the chains are run one after another, in bit-reversed
-// lane order, so the xor tree becomes a post-order walk that keeps at most log2(L) partial sums - the same additions
-// as the tree, operand for operand (fadd commutes exactly).
+// CDNA4 mapping: a workgroup owns 16 rows (their whole slab and the codebook staged in LDS once) x CT tiles of 16
+// tokens a pass. the integer half-dots are MFMAs: each 32-value block's codes (lane l: row l % 16, values 8 (l / 16) ..
+// + 7, decoded from LDS straight into its A operand - the IQ1 types' 8 grid + delta folded into one int8 per value)
+// go to two v_mfma_i32_16x16x32_i8, one with the second half's lanes zeroed, one with the first's: the two halves'
+// exact dots for 16 rows x 16 tokens. the float steps then run per output in the contract's order. the 4 waves split
+// the logical lanes (wave w the chains ll = w mod 4, blocks s = w mod 4), so a wave keeps L / 4 chains an output in
+// registers; the xor tree is finished across the waves through LDS with the same additions (fadd commutes exactly).
 #include "lanedec.h"
 
 extern "C" {
@@ -27,6 +27,7 @@ using namespace lane;
 constexpr int kWaves = 4, kThreads = kWave * kWaves;
 constexpr uint32_t kTile = 16;
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // a lane's chunk k (values 8k .. 8k + 7) of block j of a 256-value super-block: two words of int8 codes (IQ1: 8 grid +
 // delta), as codes<T> (lanedec.h) gives them for that chunk
@@ -137,43 +138,98 @@ __device__ inline void scales<kIQ1_M>(const uint8_t* b, int j, float& d, int& s0
   d = f16((a0 >> 12) | ((a1 >> 8) & 0x00F0) | ((a2 >> 4) & 0x0F00) | (a3 & 0xF000));
 }
 
-// blockIdx.x: 64 rows (a wave 16); blockIdx.y: the matrix, its cnt[m] tokens from row xrow[m] of q / d, CT tiles of
-// 16 at a time
+constexpr int kCT16 = 4, kCT32 = 2;  // token tiles a pass at 16 / 32 logical lanes (the waves' chains: 64 VGPRs)
+
+template <uint32_t T>
+constexpr uint32_t grid_bytes_of() {
+  return GridOf<T>::n * sizeof(typename GridOf<T>::E);
+}
+
+// dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the waves' scale tables and their
+// partial trees
+template <uint32_t T, int CT>
+struct Lds {
+  uint32_t slab, grid, scl, part, total;
+  __host__ __device__ Lds(uint32_t rb) {
+    slab = 0;
+    grid = (16 * rb + 15) / 16 * 16;
+    scl = grid + grid_bytes_of<T>();
+    part = scl + kWaves * 2 * kTile * 4;
+    total = part + kWaves * CT * 4 * kWave * 4;
+  }
+};
+
+// blockIdx.x: 16 rows; blockIdx.y: the matrix, its cnt[m] tokens from row xrow[m] of q / d, CT tiles of 16 a pass.
+// wave w takes the blocks s = w (mod 4): its chains are the logical lanes ll = w (mod 4), L / 4 accumulators an
+// output; the xor tree's levels L/2 .. 4 pair chains of one wave (in registers), its levels 2 and 1 pair the waves
+// (through LDS) - the same additions as the tree
 template <uint32_t T, int L, int CT>
 __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
-                                                   const int32_t* __restrict__ xrow, uint32_t rows, uint32_t cols,
+                                                   const int32_t* __restrict__ xrow, uint32_t cols,
                                                    const int8_t* __restrict__ q, const float* __restrict__ d,
                                                    float* __restrict__ y, uint32_t ys) {
-  constexpr int per = (int) (Block<T>::values / 32), kLog = L == 32 ? 5 : 4;
-  __shared__ float scl[kWaves][2][kTile];  // a block's 16 rows' ((d s21) / 8) of each half, a wave's own
+  constexpr int per = (int) (Block<T>::values / 32), C = L / kWaves;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
+  if (!n) return;  // (the whole workgroup)
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, col = lane % 16, quad = lane / 16;
-  const uint32_t row0 = blockIdx.x * kTile * kWaves + wave * kTile;
-  if (!n || row0 >= rows) return;  // (uniform: the matrix's, then the wave's; no workgroup barrier follows)
-  const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m];
-  const uint8_t* arow = w[m] + (uint64_t) (row0 + col) * row_bytes<T>(cols);  // this lane's A row
-  const auto* grid = const_grid<T>();
+  const uint32_t row0 = blockIdx.x * kTile, nblk = cols / 32, r0 = (uint32_t) xrow[m];
+  const uint32_t rb = (uint32_t) row_bytes<T>(cols);
+  const Lds<T, CT> L_(rb);
+  // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
+  {
+    const u32x4* src = (const u32x4*) (w[m] + (uint64_t) row0 * rb);
+    const uint32_t nw = 16 * rb / 16;
+    for (uint32_t i = threadIdx.x; i < nw; i += kThreads) ((u32x4*) (smem + L_.slab))[i] = src[i];
+    constexpr uint32_t ng = grid_bytes_of<T>() / 16;
+    const u32x4* gs = (const u32x4*) const_grid<T>();
+    for (uint32_t i = threadIdx.x; i < ng; i += kThreads) ((u32x4*) (smem + L_.grid))[i] = gs[i];
+  }
+  __syncthreads();
+  const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
+  float* scl = (float*) (smem + L_.scl) + wave * 2 * kTile;  // [half][row]
+  float* part = (float*) (smem + L_.part);                    // [wave][ct][i][lane]
+  const uint8_t* arow = smem + L_.slab + col * rb;            // this lane's A row
   for (uint32_t c0 = 0; c0 < n; c0 += kTile * CT) {
-    // this lane's B token in each tile (past the count: the last token, summed, never stored)
     const int8_t* xb[CT];
     const float* xd[CT];
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
+    for (int ct = 0; ct < CT; ct++) {  // this lane's B token (past the count: the last, summed, never stored)
       const uint32_t t = c0 + ct * kTile + col, tt = t < n ? t : n - 1;
       xb[ct] = q + (uint64_t) (r0 + tt) * cols + 8 * quad;
       xd[ct] = d + (uint64_t) (r0 + tt) * nblk;
     }
-    float stack[kLog][CT][4];  // the tree's pending left subtrees, level by level
-    float root[CT][4];
-    for (int p = 0; p < L; p++) {  // (uniform) chains in bit-reversed lane order
-      const uint32_t ll = __builtin_bitreverse32((uint32_t) p) >> (32 - kLog);
-      float acc[CT][4];
+    const int tiles = (int) ((n - c0 + kTile - 1) / kTile) < CT ? (int) ((n - c0 + kTile - 1) / kTile) : CT;
+    float acc[C][CT][4];
+#pragma unroll
+    for (int c = 0; c < C; c++)
 #pragma unroll
       for (int ct = 0; ct < CT; ct++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[ct][i] = 0.0f;
-      for (uint32_t s = ll; s < nblk; s += L) {
-        const uint8_t* blk = arow + (uint64_t) (s / per) * Block<T>::bytes;
+        for (int i = 0; i < 4; i++) acc[c][ct][i] = 0.0f;
+    // the activations of the wave's next block, loaded one block ahead (global memory's latency behind the MFMAs)
+    long bxn[CT];
+    float xsn[CT];
+    auto xload = [&](uint32_t s) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const uint32_t sc = s < nblk ? s : 0;
+        bxn[ct] = *(const long*) (xb[ct] + (uint64_t) sc * 32);
+        xsn[ct] = xd[ct][sc];
+      }
+    };
+    xload((uint32_t) wave);
+    for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += L) {
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const uint32_t s = s0 + kWaves * c;  // logical lane wave + 4 c
+        if (s >= nblk) break;                // (uniform)
+        long bx[CT];
+        float xs[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) bx[ct] = bxn[ct], xs[ct] = xsn[ct];
+        xload(s + kWaves);
+        const uint8_t* blk = arow + (s / per) * Block<T>::bytes;
         const int j = (int) (s % per);
         uint32_t w0, w1;
         chunk<T>(blk, j, quad, grid, w0, w1);
@@ -181,67 +237,73 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
         const long a0 = quad < 2 ? a : 0, a1 = quad < 2 ? 0 : a;  // the first half's lanes, the second's
         if (quad == 0) {  // lanes 0 .. 15: row col's ((d s21) / 8) per half (lane_part's first two products)
           float dd;
-          int s0, s1;
-          scales<T>(blk, j, dd, s0, s1);
-          scl[wave][0][col] = __fmul_rn(__fmul_rn(dd, (float) s0), 0.125f);
-          scl[wave][1][col] = __fmul_rn(__fmul_rn(dd, (float) s1), 0.125f);
+          int s0_, s1_;
+          scales<T>(blk, j, dd, s0_, s1_);
+          scl[col] = __fmul_rn(__fmul_rn(dd, (float) s0_), 0.125f);
+          scl[kTile + col] = __fmul_rn(__fmul_rn(dd, (float) s1_), 0.125f);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float f0[4], f1[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) f0[i] = scl[wave][0][4 * quad + i], f1[i] = scl[wave][1][4 * quad + i];
+        for (int i = 0; i < 4; i++) f0[i] = scl[4 * quad + i], f1[i] = scl[kTile + 4 * quad + i];
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) {
-          if (c0 + ct * kTile < n) {  // (uniform) the tiles that exist
-            const long bx = *(const long*) (xb[ct] + (uint64_t) s * 32);
-            const v4i I0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bx, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const v4i I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bx, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const float xs = xd[ct][s];
+          if (ct < tiles) {
+            const v4i I0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bx[ct], v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bx[ct], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
               const float sub = __fadd_rn(__fmul_rn(f0[i], (float) I0[i]), __fmul_rn(f1[i], (float) I1[i]));
-              acc[ct][i] = __builtin_fmaf(xs, sub, acc[ct][i]);
+              acc[c][ct][i] = __builtin_fmaf(xs[ct], sub, acc[c][ct][i]);
             }
           }
         }
         __builtin_amdgcn_wave_barrier();  // the table read by every lane before the next block's is written
       }
-      // the chain's sum into the tree: position p's leaf, merged with each complete left sibling
+    }
+    // the tree's levels L/2 .. 4 within the wave: chains c and c ^ o4 (logical lanes ll and ll ^ 4 o4)
 #pragma unroll
-      for (int ct = 0; ct < CT; ct++)
+    for (int o4 = C / 2; o4 > 0; o4 >>= 1)
+#pragma unroll
+      for (int c = 0; c < o4; c++)
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[c][ct][i] = __fadd_rn(acc[c][ct][i], acc[c + o4][ct][i]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) part[((wave * CT + ct) * 4 + i) * kWave + lane] = acc[0][ct][i];
+    __syncthreads();
+    if (wave == 0) {  // levels 2 and 1: (T0 + T2) + (T1 + T3), T_w the wave's subtree (logical lanes w mod 4)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const uint32_t t = c0 + ct * kTile + col;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          float v = acc[ct][i];
-          bool open = true;
-#pragma unroll
-          for (int lv = 0; lv < kLog; lv++)
-            if (open) {
-              if ((p >> lv) & 1) v = __fadd_rn(stack[lv][ct][i], v);
-              else stack[lv][ct][i] = v, open = false;
-            }
-          if (open) root[ct][i] = v;  // p = L - 1: the whole tree
+          const float* pp = part + (ct * 4 + i) * kWave + lane;
+          const uint32_t wv = CT * 4 * kWave;  // a wave's stride
+          const float v = __fadd_rn(__fadd_rn(pp[0], pp[2 * wv]), __fadd_rn(pp[wv], pp[3 * wv]));
+          if (t < n) y[(uint64_t) (r0 + t) * ys + row0 + 4 * quad + i] = v;
         }
+      }
     }
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
-      const uint32_t t = c0 + ct * kTile + col;
-      if (t < n)
-#pragma unroll
-        for (int i = 0; i < 4; i++) y[(uint64_t) (r0 + t) * ys + row0 + 4 * quad + i] = root[ct][i];
-    }
+    __syncthreads();  // the partial trees read before the next pass writes them
   }
 }
 
-template <uint32_t T, int L>
-bool by_tiles(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t max_cnt,
-              uint32_t rows, uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
-  const dim3 grid((rows + kTile * kWaves - 1) / (kTile * kWaves), n_mat);
-  if (max_cnt <= kTile)
-    kernel<T, L, 1><<<grid, kThreads, 0, s>>>((const uint8_t* const*) w, cnt, xrow, rows, cols, q, d, y, ys);
-  else
-    kernel<T, L, 2><<<grid, kThreads, 0, s>>>((const uint8_t* const*) w, cnt, xrow, rows, cols, q, d, y, ys);
+template <uint32_t T, int L, int CT>
+bool launch(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t rows,
+            uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
+  const Lds<T, CT> l((uint32_t) row_bytes<T>(cols));
+  if (l.total > 160 * 1024) return false;
+  auto k = kernel<T, L, CT>;
+  if (l.total > 64 * 1024 &&
+      hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
+    return false;
+  k<<<dim3(rows / kTile, n_mat), kThreads, l.total, s>>>((const uint8_t* const*) w, cnt, xrow, cols, q, d, y, ys);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -249,8 +311,9 @@ template <uint32_t T>
 bool by_lanes(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t max_cnt,
               uint32_t rows, uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
   if (cols % Block<T>::values) return false;
-  return cols >= 4096 ? by_tiles<T, 32>(w, cnt, xrow, n_mat, max_cnt, rows, cols, q, d, y, ys, s)
-                      : by_tiles<T, 16>(w, cnt, xrow, n_mat, max_cnt, rows, cols, q, d, y, ys, s);
+  (void) max_cnt;
+  return cols >= 4096 ? launch<T, 32, kCT32>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s)
+                      : launch<T, 16, kCT16>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s);
 }
 
 }  // namespace lgemm
