@@ -19,8 +19,15 @@ namespace fused {
 
 using namespace lane;
 
-constexpr int kGuThreads = 256, kDnThreads = 1024;  // a gate/up tile's workgroup, a down tile's
-constexpr uint32_t kGuRows = 4, kDnRows = 8, kMaxTok = 64, kMaxK = 32;
+// a gate/up tile's workgroup and rows: small tiles for one token (latency: every CU busy, no tail), larger for a
+// batch (each decoded block serves several tokens); a down tile's
+template <int NT>
+struct GuShape {
+  static constexpr int threads = NT == 1 ? 256 : 512;
+  static constexpr uint32_t rows = NT == 1 ? 4 : 8;
+};
+constexpr int kDnThreads = 1024;
+constexpr uint32_t kGuRowsMax = 8, kDnRows = 8, kMaxTok = 64, kMaxK = 32;
 
 __host__ __device__ constexpr uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
@@ -29,6 +36,7 @@ struct GuLds {
   uint32_t wg, wu, q, d, grid, toks, ids, subs, gv, total;
 };
 __host__ __device__ inline GuLds gu_lds(uint32_t row_bytes, uint32_t dim, int nt, uint32_t grid_bytes, uint32_t n) {
+  const uint32_t kGuRows = nt == 1 ? GuShape<1>::rows : GuShape<2>::rows;
   GuLds l;
   uint32_t at = 0;
   l.wg = at, at += align16(kGuRows * row_bytes);
@@ -228,9 +236,11 @@ __device__ __forceinline__ void grid_store(const GridStage<T, NTH>& g, uint8_t* 
 __device__ inline float tree_rt(float v, int L) { return L == 32 ? tree<32>(v) : tree<16>(v); }
 
 // one gate/up tile: expert of pick m (its first pick's tile: others return at once), rows tile * kGuRows .. + kGuRows
+// (GuShape<NT>::rows)
 template <uint32_t T, int NT>
 __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t tile, uint8_t* smem, int L) {
-  constexpr int kThreads = kGuThreads;
+  constexpr int kThreads = GuShape<NT>::threads;
+  constexpr uint32_t kGuRows = GuShape<NT>::rows;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t r0 = tile * kGuRows, n = a.n_tok * a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
@@ -356,7 +366,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   }
 }
 
-// one down tile: token t, rows tile * kGuRows .. + kGuRows
+// one down tile: token t, rows tile * kDnRows .. + kDnRows
 template <uint32_t T>
 __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, int L) {
   constexpr int kThreads = kDnThreads;
@@ -446,7 +456,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
 }
 
 template <uint32_t T, int NT, int L>
-__global__ __launch_bounds__(kGuThreads) void gu_kernel(GuArgs a) {
+__global__ __launch_bounds__(GuShape<NT>::threads) void gu_kernel(GuArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, L);
 }

@@ -23,7 +23,7 @@ bool gu_launch(const GuArgs& a, hipStream_t s) {
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
-  k<<<dim3(a.ff / fused::kGuRows, n), fused::kGuThreads, l.total, s>>>(a);
+  k<<<dim3(a.ff / fused::GuShape<NT>::rows, n), fused::GuShape<NT>::threads, l.total, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -91,7 +91,7 @@ extern "C" OSM_API uint64_t osmos_lane_workspace(const OsmosLaneLayer* L, uint32
 namespace {
 bool layer_ok(const OsmosLaneLayer* L, uint32_t n_tok) {
   return L && n_tok && L->k && L->dim && L->ff && L->n_exp && L->gate && L->up && L->down && n_tok <= fused::kMaxTok &&
-         L->k <= fused::kMaxK && L->dim % 32 == 0 && L->ff % fused::kGuRows == 0 && L->ff % 32 == 0 &&
+         L->k <= fused::kMaxK && L->dim % 32 == 0 && L->ff % fused::kGuRowsMax == 0 && L->ff % 32 == 0 &&
          L->dim % fused::kDnRows == 0 &&
          ((uintptr_t) L->gate | (uintptr_t) L->up | (uintptr_t) L->down | L->gate_bytes | L->up_bytes | L->down_bytes) %
                  16 == 0;
