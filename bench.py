@@ -339,7 +339,7 @@ def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=
 
 
 def half_bench(torch, capi, lay, half, reps=20):
-    """one fused kernel of the layer alone: osmos_lane_gate_up (fused::gu_kernel) or osmos_lane_down (fused::dn_kernel)
+    """one fused kernel of the layer alone: osmos_lane_gate_up (fused::gu1_kernel at one token) or osmos_lane_down (fused::dn_kernel)
     over the timed steps' routing and rotated weights, G launches back to back in a graph on stream s; the average
     duration a launch from events recorded on s; its algorithmic bytes (each distinct expert's matrices once, the
     activations in, the outputs out)"""
@@ -476,13 +476,13 @@ def main():
                    "pct_hbm_peak": round(100 * lay["gbs"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(ker["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ker["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "osm::fused::gu_kernel<IQ3_XXS,1,16>", "us_per_launch": round(ker["us"], 3),
+                     "kernel": "osm::fused::gu1_kernel<IQ3_XXS,16>", "us_per_launch": round(ker["us"], 3),
                      "bytes_per_launch": int(ker["bytes"])},
         "kernels": {"osm::fused::dn_kernel<IQ3_XXS,16>": {"us_per_launch": round(dn["us"], 3),
                                                           "bytes_per_launch": int(dn["bytes"]),
                                                           "GB/s": round(dn["gbs"], 2)}},
     }
-    traffic = os.path.join(ROOT, "profiles", "gu_kernel_iq3xxs_bs1_traffic.json")
+    traffic = os.path.join(ROOT, "profiles", "gu1_kernel_iq3xxs_bs1_traffic.json")
     if os.path.exists(traffic):  # HBM bytes a launch, from the counter runs that file records
         with open(traffic) as f:
             line["roofline"]["traffic"] = json.load(f)["hbm_bytes_per_launch"]

@@ -1,11 +1,12 @@
-// libosmos MI355X - the routed layer's two fused kernels (osmos_lane_layer, layer.hip), bit for bit the lane
-// contract's sums in the reference's layer order (src/cpu/lane.c:98-118, src/run/hip_lane.c:164-220):
+// libosmos MI355X - the routed layer's fused kernels (osmos_lane_layer, layer.hip), bit for bit the lane contract's
+// sums in the reference's layer order (src/cpu/lane.c:98-118, src/run/hip_lane.c:164-220):
 //
-// gu_kernel (gate/up): a workgroup is (an expert, a tile of 16 of its ff rows). its expert's first pick owns it: the
-//   picks that chose the same expert (at most one a token) are its tokens, read once for all of them. it stages the
-//   tile's gate and up rows in LDS with 16-byte loads (every load issued before any is waited on), copies the type's
-//   codebook to LDS, rounds its tokens' x rows itself (q8_round's bits), then each row's lane sums, the tree and
-//   lane_swiglu(gate, up, lim, w[pick]) into h[pick][row].
+// gu1_kernel (gate/up, one token: decode): a workgroup is (a pick, a tile of 4 of its ff rows). the pick's expert id
+//   is a scalar load; the codebook and the token's x are issued before it is waited for, the tile's gate and up rows
+//   right after (one scalar base a matrix). x is rounded in LDS (q8_round's bits), then each row's lane sums, the
+//   tree and lane_swiglu(gate, up, lim, w[pick]) into h[pick][row].
+// gu_kernel (gate/up, a batch): a workgroup is (an expert, a tile of 8 of its ff rows). its expert's first pick owns
+//   it: the picks that chose the same expert (at most one a token) are its tokens, read once for all of them.
 // dn_kernel (down): a workgroup is (a token, a tile of 8 of the dim rows). it rounds h of the token's k picks into LDS
 //   (q8_round's bits), stages the k experts' tile rows, sums each (expert, row) in the lane order, then each row's k
 //   sums in ascending expert id (the reference's ops_gather_sum_add order) and add[t][row] after.
@@ -46,7 +47,7 @@ __host__ __device__ inline GuLds gu_lds(uint32_t row_bytes, uint32_t dim, int nt
   l.grid = at, at += align16(grid_bytes);
   l.toks = at, at += align16((2 * kMaxTok + 1) * 4);
   l.ids = at, at += align16(n * 4);
-  l.subs = at, at += align16(2 * (uint32_t) nt * kGuRows * (dim / 32) * 4);
+  l.subs = at, at += align16(2 * (uint32_t) nt * kGuRows * (dim / 32 + 1) * 4);
   l.gv = at, at += align16(2 * (uint32_t) nt * kGuRows * 4);
   l.total = at;
   return l;
@@ -65,7 +66,7 @@ __host__ __device__ inline DnLds dn_lds(uint32_t row_bytes, uint32_t ff, uint32_
   l.grid = at, at += align16(grid_bytes);
   l.ye = at, at += align16(k * kDnRows * 4);
   l.picks = at, at += align16(2 * kMaxK * 4);
-  l.subs = at, at += align16(k * kDnRows * (ff / 32) * 4);
+  l.subs = at, at += align16(k * kDnRows * (ff / 32 + 1) * 4);
   l.total = at;
   return l;
 }
@@ -195,32 +196,67 @@ __device__ __forceinline__ void round_store(const Rounded& r, uint32_t blocks, u
 
 
 // the codebook (1 - 16 KB of constant memory, 16-aligned): grid_load() issues its loads into registers, grid_store()
-// writes them to the workgroup's LDS copy - apart, so the loads can be issued first and waited for last
-template <uint32_t T, int NTH>
+// writes them to the workgroup's LDS copy - apart, so the loads can be issued first and waited for last. IQ3_XXS's
+// signed table (16 KB) is not loaded: its 256 grid words (1 KB) are, and each is expanded in LDS to its 16 sign
+// variants - variant s of word g takes byte i from -g where bit i of s is set, from g otherwise (one byte permute
+// each), 16 g + s as the lookups index it. (the table's address is passed through an empty asm: its loads are then
+// ordinary global loads, issued where they are written rather than moved next to their use)
+template <uint32_t T, int NTH, bool Expand = true>
 struct GridStage {
-  static constexpr uint32_t n = grid_bytes<T>() / 16, per = (n + NTH - 1) / NTH;
-  u32x4 v[per > 0 ? per : 1];
+  static constexpr bool expand = Expand && T == kIQ3_XXS;
+  static constexpr uint32_t n = expand ? 256 : grid_bytes<T>() / 16, words = expand ? 1 : 4;
+  static constexpr uint32_t per = (n + NTH - 1) / NTH;
+  // expanding, a thread takes grid word (u NTH + threadIdx.x) % 256 and `quads` of its 4 groups of 4 variants
+  static constexpr uint32_t quads = NTH >= 1024 ? 1 : 1024 / NTH;
+  static_assert(!expand || NTH >= 256 && NTH <= 1024 && NTH % 256 == 0, "the expansion's thread split");
+  uint32_t v[per > 0 ? per * words : 1];
 };
-template <uint32_t T, int NTH>
-__device__ __forceinline__ void grid_load(GridStage<T, NTH>& g) {
-  constexpr uint32_t n = GridStage<T, NTH>::n;
-  if constexpr (n > 0) {
-    const u32x4* src = (const u32x4*) const_grid<T>();
+typedef const __attribute__((address_space(1))) uint32_t* gptr32;
+typedef const __attribute__((address_space(1))) u32x4* gptr128;
+template <typename P, typename Q>
+__device__ __forceinline__ P opaque_global(const Q* p) {
+  uint64_t v = (uint64_t) p;
+  asm volatile("" : "+s"(v));
+  return (P) v;
+}
+template <uint32_t T, int NTH, bool E>
+__device__ __forceinline__ void grid_load(GridStage<T, NTH, E>& g) {
+  using G = GridStage<T, NTH, E>;
+  if constexpr (G::expand) {
+    const gptr32 src = opaque_global<gptr32>(kGrids.iq3xxs);
+    g.v[0] = src[threadIdx.x % 256];
+  } else if constexpr (G::n > 0) {
+    const gptr128 src = opaque_global<gptr128>(const_grid<T>());
 #pragma unroll
-    for (uint32_t u = 0; u < GridStage<T, NTH>::per; u++) {
+    for (uint32_t u = 0; u < G::per; u++) {
       const uint32_t l = u * NTH + threadIdx.x;
-      g.v[u] = src[l < n ? l : 0];
+      const u32x4 w = src[l < G::n ? l : 0];
+      g.v[4 * u] = w.x, g.v[4 * u + 1] = w.y, g.v[4 * u + 2] = w.z, g.v[4 * u + 3] = w.w;
     }
   }
 }
-template <uint32_t T, int NTH>
-__device__ __forceinline__ void grid_store(const GridStage<T, NTH>& g, uint8_t* lds) {
-  constexpr uint32_t n = GridStage<T, NTH>::n;
-  if constexpr (n > 0) {
+template <uint32_t T, int NTH, bool E>
+__device__ __forceinline__ void grid_store(const GridStage<T, NTH, E>& g, uint8_t* lds) {
+  using G = GridStage<T, NTH, E>;
+  if constexpr (G::expand) {
+    const uint32_t pos = g.v[0], neg = ~pos + 0x01010101u;  // (bytes 4 .. 62: no borrow between bytes)
+    const uint32_t q0 = (threadIdx.x / 256) * G::quads;
+    u32x4* dst = (u32x4*) lds + 4 * (threadIdx.x % 256) + q0;
 #pragma unroll
-    for (uint32_t u = 0; u < GridStage<T, NTH>::per; u++) {
+    for (uint32_t qq = 0; qq < G::quads; qq++) {
+      const uint32_t hi = (q0 + qq) * 4;  // (variants 4 (q0 + qq) .. + 3: bits 2, 3 of the variant)
+      const uint32_t sh = (hi >> 2 & 1) * 0x040000u + (hi >> 3 & 1) * 0x04000000u;
+      uint32_t w[4];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++)
+        w[i] = __builtin_amdgcn_perm(neg, pos, 0x03020100u + (i & 1) * 0x04u + (i >> 1) * 0x0400u + sh);
+      dst[qq] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  } else if constexpr (G::n > 0) {
+#pragma unroll
+    for (uint32_t u = 0; u < G::per; u++) {
       const uint32_t l = u * NTH + threadIdx.x;
-      if (l < n) ((u32x4*) lds)[l] = g.v[u];
+      if (l < G::n) ((u32x4*) lds)[l] = u32x4{g.v[4 * u], g.v[4 * u + 1], g.v[4 * u + 2], g.v[4 * u + 3]};
     }
   }
 }
@@ -247,8 +283,8 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   const GuLds L_ = gu_lds(rb, a.dim, NT, grid_bytes<T>(), n);
   int32_t* toks = (int32_t*) (smem + L_.toks);  // [0, kMaxTok): the expert's picks in token order; [2 kMaxTok]: count
   // loads that need no routing first: the codebook and, for one token, its x row (the pick's own token)
-  GridStage<T, kThreads> gs;
-  grid_load<T, kThreads>(gs);
+  GridStage<T, kThreads, false> gs;  // (the full table: the batch tiles' loads are not what bounds them)
+  grid_load(gs);
   Rounded rx;
   if constexpr (NT == 1) {
     const float* xrow = a.x + (uint64_t) (m / a.k) * a.dim;
@@ -281,6 +317,9 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
   }
   __syncthreads();
   const int cnt = __builtin_amdgcn_readfirstlane(toks[2 * kMaxTok]);
+  // the first chunk's router weights, loaded now so that their latency is not the tile's last step
+  float w0 = 0.0f;
+  if (threadIdx.x < NT * kGuRows && (int) threadIdx.x / (int) kGuRows < cnt) w0 = a.w[toks[threadIdx.x / kGuRows]];
   int8_t* q = (int8_t*) (smem + L_.q);
   float* d = (float*) (smem + L_.d);
   // one round of loads: the tile's gate and up rows (contiguous in each tensor), the codebook, the first chunk's x
@@ -301,7 +340,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
     Staged st;
     stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, 0);
     if constexpr (NT > 1) round_load<kThreads>(rx, xval(live0, 0), xblocks, 0);
-    grid_store<T, kThreads>(gs, smem + L_.grid);
+    grid_store(gs, smem + L_.grid);
     round_store<kThreads>(rx, xblocks, 0, nblk, a.dim, q, d);
     stage_store<kThreads>(st, smem + L_.wg, nw, 0);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {  // (tiles past one round)
@@ -340,7 +379,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
         const int4* xp = (const int4*) (q + t * a.dim + s * 32);
         const int4 x0 = xp[0], x1 = xp[1];
         x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
-        subs[((mm * NT + t) * kGuRows + row) * nblk + s] = block_sum<T>(c, x);
+        subs[((mm * NT + t) * kGuRows + row) * (nblk + 1) + s] = block_sum<T>(c, x);
       }
     }
     __syncthreads();
@@ -348,7 +387,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
     const uint32_t chains = 2 * NT * kGuRows * L, lgL = L == 32 ? 5 : 4;
     for (uint32_t ch = threadIdx.x; ch < (chains + kWave - 1) / kWave * kWave; ch += kThreads) {
       const uint32_t ll = ch & (L - 1), unit = (ch >> lgL) < 2 * NT * kGuRows ? ch >> lgL : 0, t = (unit / kGuRows) % NT;
-      const float* sb = subs + unit * nblk;
+      const float* sb = subs + unit * (nblk + 1);
       float acc = 0.0f;
       for (uint32_t s = ll; s < nblk; s += L) acc = __builtin_fmaf(d[t * nblk + s], sb[s], acc);
       const float v = tree_rt(acc, L);
@@ -360,7 +399,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
       if (t < live) {
         const int pk = toks[c0 + t];
         a.h[(uint64_t) pk * a.ff + r0 + row] =
-            lane_swiglu(gv[t * kGuRows + row], gv[(NT + t) * kGuRows + row], a.lim, a.w[pk]);
+            lane_swiglu(gv[t * kGuRows + row], gv[(NT + t) * kGuRows + row], a.lim, c0 ? a.w[pk] : w0);
       }
     }
   }
@@ -382,8 +421,10 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   const uint32_t hblocks = K * nblk;
   Rounded rh;
   round_load<kThreads>(rh, hval, hblocks, 0);
-  GridStage<T, kThreads> gs;
-  grid_load<T, kThreads>(gs);
+  const uint64_t o = (uint64_t) t * a.dim + r0 + threadIdx.x;
+  const float addv = threadIdx.x < kDnRows ? a.add[o] : 0.0f;  // (loaded now: its latency off the tile's end)
+  GridStage<T, kThreads, false> gs;  // (the full table: expanding it in 4 of the 16 waves is slower here)
+  grid_load(gs);
   int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: pick j's expert; [kMaxK + r]: the pick j of rank r
   if (threadIdx.x < K) picks[threadIdx.x] = a.ids[t * K + threadIdx.x];
   __syncthreads();
@@ -407,7 +448,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
       }
       if (j < K) picks[kMaxK + rank] = (int32_t) j;
     }
-    grid_store<T, kThreads>(gs, smem + L_.grid);
+    grid_store(gs, smem + L_.grid);
     round_store<kThreads>(rh, hblocks, 0, nblk, a.ff, q, d);
     stage_store<kThreads>(st, smem + L_.w, nw, 0);
     for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {
@@ -433,14 +474,14 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
     const int4* xp = (const int4*) (q + j * a.ff + s * 32);
     const int4 x0 = xp[0], x1 = xp[1];
     x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
-    subs[(j * kDnRows + row) * nblk + s] = block_sum<T>(c, x);
+    subs[(j * kDnRows + row) * (nblk + 1) + s] = block_sum<T>(c, x);
   }
   __syncthreads();
   // phase B: a chain a (pick, row, logical lane)
   const uint32_t chains = K * kDnRows * L, lgL = L == 32 ? 5 : 4;
   for (uint32_t ch = threadIdx.x; ch < (chains + kWave - 1) / kWave * kWave; ch += kThreads) {
     const uint32_t ll = ch & (L - 1), unit = (ch >> lgL) < K * kDnRows ? ch >> lgL : 0, j = unit / kDnRows;
-    const float* sb = subs + unit * nblk;
+    const float* sb = subs + unit * (nblk + 1);
     float acc = 0.0f;
     for (uint32_t s = ll; s < nblk; s += L) acc = __builtin_fmaf(d[j * nblk + s], sb[s], acc);
     const float v = tree_rt(acc, L);
@@ -450,8 +491,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   if (threadIdx.x < kDnRows) {  // each row's k sums in ascending expert id, then add's
     float s = 0.0f;
     for (uint32_t r = 0; r < K; r++) s = __fadd_rn(s, ye[picks[kMaxK + r] * kDnRows + threadIdx.x]);
-    const uint64_t o = (uint64_t) t * a.dim + r0 + threadIdx.x;
-    a.out[o] = __fadd_rn(s, a.add[o]);
+    a.out[o] = __fadd_rn(s, addv);
   }
 }
 
@@ -459,6 +499,106 @@ template <uint32_t T, int NT, int L>
 __global__ __launch_bounds__(GuShape<NT>::threads) void gu_kernel(GuArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, L);
+}
+
+// gu1_kernel: the one-token gate/up (decode) - gu_kernel's tile for a token alone, its loads issued with no work
+// between the expert id's arrival and the weights' issue: each 16-byte word's offset in its matrix's kG1Rows rows is
+// set before the id is waited for, the rows' bases are scalar (the id is a scalar load), and every staging slot holds
+// one matrix's words, so a slot's loads are one scalar base plus the lane's offset. workgroup (tile, pick m): rows
+// kG1Rows tile .. of the gate and up matrices of expert ids[m]; then phase A and B as gu_kernel's and
+// lane_swiglu(gate, up, lim, w[m]) into h[m][row].
+constexpr int kG1Threads = GuShape<1>::threads;
+constexpr uint32_t kG1Rows = GuShape<1>::rows;
+constexpr uint32_t kG1Slots = kPer / 2;  // staging slots a matrix: its rows at most kG1Slots kG1Threads words
+
+// gu1_kernel's LDS: the codebook first (its lookups need no base), x's codes and scales, the gate and up rows, sums
+struct G1Lds {
+  uint32_t grid, q, d, w, subs, total;
+};
+__host__ __device__ inline G1Lds g1_lds(uint32_t row_bytes, uint32_t dim, uint32_t grid_bytes) {
+  G1Lds l;
+  uint32_t at = 0;
+  l.grid = at, at += align16(grid_bytes);
+  l.q = at, at += align16(dim);
+  l.d = at, at += align16((dim / 32) * 4);
+  l.w = at, at += align16(2 * kG1Rows * row_bytes);
+  l.subs = at, at += align16(2 * kG1Rows * (dim / 32 + 1) * 4);
+  l.total = at;
+  return l;
+}
+
+template <uint32_t T, int L>
+__global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int kThreads = kG1Threads;
+  constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
+  const uint32_t m = blockIdx.y, r0 = blockIdx.x * kG1Rows;
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
+  const G1Lds L_ = g1_lds(rb, a.dim, grid_bytes<T>());
+  const uint32_t per_seg = kG1Rows * rb / 16;  // a matrix's words
+  // the lane's word of each slot (past the matrix's end: its last word again, loaded and not stored)
+  uint32_t idx[kG1Slots];
+#pragma unroll
+  for (uint32_t u = 0; u < kG1Slots; u++) idx[u] = min(u * kThreads + threadIdx.x, per_seg - 1);
+  const uint32_t e = (uint32_t) a.ids[m];  // (an expert id: not negative; unsigned, so no sign extension to wait for)
+  const float wm = a.w[m];
+  GridStage<T, kThreads> gs;
+  grid_load(gs);
+  Rounded rx;  // (the one token's row)
+  round_load<kThreads>(rx, [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) { return a.x + blk * 32 + i; },
+                       nblk, 0);
+  // (a scheduling barrier: the codebook and x loads issue before the id is waited for)
+  __builtin_amdgcn_sched_barrier(0);
+  const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
+  const u32x4* usrc = (const u32x4*) (a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb);
+  u32x4 wv[2 * kG1Slots];
+#pragma unroll
+  for (uint32_t u = 0; u < kG1Slots; u++) wv[u] = gsrc[idx[u]], wv[kG1Slots + u] = usrc[idx[u]];
+  int8_t* q = (int8_t*) (smem + L_.q);
+  float* d = (float*) (smem + L_.d);
+  grid_store(gs, smem + L_.grid);
+  round_store<kThreads>(rx, nblk, 0, nblk, a.dim, q, d);
+#pragma unroll
+  for (uint32_t u = 0; u < kG1Slots; u++) {
+    const uint32_t l = u * kThreads + threadIdx.x;
+    if (l < per_seg) {
+      ((u32x4*) (smem + L_.w))[l] = wv[u];
+      ((u32x4*) (smem + L_.w))[per_seg + l] = wv[kG1Slots + u];
+    }
+  }
+  __syncthreads();
+  const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
+  float* subs = (float*) (smem + L_.subs);  // [unit][s], unit = kG1Rows matrix + row
+  // phase A: (block, unit) items, the unit fastest: the units of a block share its x
+  constexpr uint32_t U = 2 * kG1Rows;
+  const uint32_t items = U * nblk;
+  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
+    const uint32_t unit = it % U, sb = it / U;
+    Codes c;
+    codes<T>(smem + L_.w + unit * rb + (sb / per) * bb, (int) (sb % per), c, grid);
+    int x[8];
+    load_x(q, sb * 32, x);
+    subs[unit * (nblk + 1) + sb] = block_sum<T>(c, x);
+  }
+  __syncthreads();
+  // phase B, in wave 0 alone (no more barriers): lane l is logical lane l % L of rows l / L + (64 / L) i; for each,
+  // the gate and up chains and trees, then lane_swiglu from the group's first lane
+  if (threadIdx.x < kWave) {
+    const uint32_t ll = threadIdx.x % L;
+#pragma unroll
+    for (uint32_t i = 0; i < kG1Rows * L / kWave; i++) {
+      const uint32_t row = threadIdx.x / L + (kWave / L) * i;
+      const float* sg = subs + row * (nblk + 1);
+      const float* su = subs + (kG1Rows + row) * (nblk + 1);
+      float ag = 0.0f, au = 0.0f;
+      for (uint32_t s = ll; s < nblk; s += L) {
+        const float xd = d[s];
+        ag = __builtin_fmaf(xd, sg[s], ag), au = __builtin_fmaf(xd, su[s], au);
+      }
+      const float g = tree<L>(ag), u = tree<L>(au);
+      if (ll == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);
+    }
+  }
 }
 
 template <uint32_t T, int L>

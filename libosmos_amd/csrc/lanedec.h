@@ -244,6 +244,15 @@ template <uint32_t T>
 __device__ inline float block_sum(const Codes& c, const int* x) {
   using Tr = Traits<T>;
   int isum[2], xsum[2];
+  if constexpr (!Tr::iq1 && !Tr::has_min && !Tr::bias) {  // a half's 4 dots in one chain (the same integer)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int s = 0;
+#pragma unroll
+      for (int i = 4 * h; i < 4 * h + 4; i++) s = dot4(c.w[i], x[i], s);
+      isum[h] = s, xsum[h] = 0;
+    }
+  } else
 #pragma unroll
   for (int h = 0; h < 2; h++) {
     int s = 0, sx = 0;

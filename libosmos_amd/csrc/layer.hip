@@ -27,6 +27,21 @@ bool gu_launch(const GuArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess;
 }
 
+// the one-token gate/up, when a matrix's tile rows fit its staging slots (false: not taken, the caller uses gu_kernel)
+template <uint32_t T, int L>
+bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
+  *taken = false;
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim);
+  if ((fused::kG1Rows * rb) % 16 || fused::kG1Rows * rb / 16 > fused::kG1Slots * fused::kG1Threads ||
+      a.dim / 32 > fused::kRoundBlocks<fused::kG1Threads> || a.ff % fused::kG1Rows)
+    return true;
+  const fused::G1Lds l = fused::g1_lds(rb, a.dim, fused::grid_bytes<T>());
+  if (l.total > 64 * 1024) return true;
+  *taken = true;
+  fused::gu1_kernel<T, L><<<dim3(a.ff / fused::kG1Rows, a.k), fused::kG1Threads, l.total, s>>>(a);
+  return hipGetLastError() == hipSuccess;
+}
+
 template <uint32_t T, int L>
 bool dn_launch(const DnArgs& a, hipStream_t s) {
   const fused::DnLds l = fused::dn_lds((uint32_t) row_bytes<T>(a.ff), a.ff, a.k, fused::grid_bytes<T>());
@@ -43,7 +58,12 @@ template <uint32_t T>
 bool gu_by(const GuArgs& a, hipStream_t s) {
   if (a.dim % Block<T>::values) return false;
   const bool wide = a.dim >= 4096;  // the contract's 32 lanes a row
-  if (a.n_tok == 1) return wide ? gu_launch<T, 1, 32>(a, s) : gu_launch<T, 1, 16>(a, s);
+  if (a.n_tok == 1) {
+    bool taken = false;
+    const bool ok = wide ? gu1_launch<T, 32>(a, s, &taken) : gu1_launch<T, 16>(a, s, &taken);
+    if (taken) return ok;
+    return wide ? gu_launch<T, 1, 32>(a, s) : gu_launch<T, 1, 16>(a, s);
+  }
   return wide ? gu_launch<T, 2, 32>(a, s) : gu_launch<T, 2, 16>(a, s);
 }
 

@@ -250,6 +250,31 @@ def test_lane_layer_deepseek_shape(g, name, n_tok):
     assert (g.bits(g.host(out)) == g.bits(want)).all()
 
 
+@pytest.mark.parametrize("name", ["IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ1_S", "IQ1_M", "Q2_K", "Q4_0", "Q4_K", "Q3_K"])
+def test_lane_layer_one_token_types(g, name):
+    """a single token (the decode kernels: one gate/up tile a workgroup) for every lane type, dim 2048 (16 lanes a row)
+    and 4096 (32), with a finite clamp: the oracle's bits"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t = synth.ID[name]
+    for dim, ff in ((2048, 256), (4096, 512)):
+        n_exp, k = 12, 5
+        mk = synth.iq_blocks if name.startswith("IQ") else synth.random_blocks
+        gate = [mk(t, ff, dim, 400 + e) for e in range(n_exp)]
+        up = [mk(t, ff, dim, 500 + e) for e in range(n_exp)]
+        down = [mk(t, dim, ff, 600 + e) for e in range(n_exp)]
+        rng = np.random.default_rng(dim)
+        x = rng.normal(0, 1, (1, dim)).astype(np.float32)
+        ids, wts = _route(rng, 1, n_exp, k)
+        want = _lane_layer_oracle(t, x, ids, wts, gate, up, down, dim, ff, 1.5)
+        D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+        L = LaneLayer(t, t, dim, ff, n_exp, k, D(gate), D(up), D(down), lim=1.5)
+        out = torch.full((1, dim), float("nan"), device="cuda")
+        print("one-token layer", name, dim, flush=True)
+        L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((1, dim), device="cuda"), out)
+        assert (g.bits(g.host(out)) == g.bits(want)).all(), (name, dim)
+
+
 def _layer_case(tg, td, n_exp, k, dim, ff, seed):
     gate = [synth.iq_blocks(tg, ff, dim, seed + 1000 + e) for e in range(n_exp)]
     up = [synth.iq_blocks(tg, ff, dim, seed + 2000 + e) for e in range(n_exp)]
