@@ -53,9 +53,9 @@ __host__ __device__ inline GuLds gu_lds(uint32_t row_bytes, uint32_t dim, int nt
   return l;
 }
 
-// dn_kernel's LDS: the k experts' tiles, the k rounded h rows and scales, the k row sums, the sorted picks
+// dn_kernel's LDS: the k experts' tiles, the k rounded h rows and scales, the codebook, the row sums, the sorted picks
 struct DnLds {
-  uint32_t w, q, d, grid, ye, picks, subs, total;
+  uint32_t w, q, d, grid, ye, picks, total;
 };
 __host__ __device__ inline DnLds dn_lds(uint32_t row_bytes, uint32_t ff, uint32_t k, uint32_t grid_bytes) {
   DnLds l;
@@ -66,7 +66,6 @@ __host__ __device__ inline DnLds dn_lds(uint32_t row_bytes, uint32_t ff, uint32_
   l.grid = at, at += align16(grid_bytes);
   l.ye = at, at += align16(k * kDnRows * 4);
   l.picks = at, at += align16(2 * kMaxK * 4);
-  l.subs = at, at += align16(k * kDnRows * (ff / 32 + 1) * 4);
   l.total = at;
   return l;
 }
@@ -125,9 +124,9 @@ __device__ __forceinline__ void unroll(F&& f) {
     unroll<N, U + 1>(f);
   }
 }
-template <int NTH, typename Src>
+template <int NTH, int S = kPer, typename Src>
 __device__ __forceinline__ void stage_load(Staged& st, Src src, uint32_t n, uint32_t per_seg, float inv, uint32_t base) {
-  unroll<kPer>([&](auto u) __attribute__((always_inline)) {
+  unroll<S>([&](auto u) __attribute__((always_inline)) {
     const uint32_t l0 = base + u.value * NTH + threadIdx.x, l = l0 < n ? l0 : 0;  // (past the end: word 0 again)
     uint32_t j = (uint32_t) ((float) l * inv);
     j -= j * per_seg > l;
@@ -135,9 +134,9 @@ __device__ __forceinline__ void stage_load(Staged& st, Src src, uint32_t n, uint
     st.template at<u.value>() = ((const u32x4*) src(j))[l - j * per_seg];
   });
 }
-template <int NTH>
+template <int NTH, int S = kPer>
 __device__ __forceinline__ void stage_store(const Staged& st, uint8_t* lds, uint32_t n, uint32_t base) {
-  unroll<kPer>([&](auto u) __attribute__((always_inline)) {
+  unroll<S>([&](auto u) __attribute__((always_inline)) {
     const uint32_t l = base + u.value * NTH + threadIdx.x;
     if (l < n) ((u32x4*) lds)[l] = st.template at<u.value>();
   });
@@ -406,7 +405,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
 }
 
 // one down tile: token t, rows tile * kDnRows .. + kDnRows
-template <uint32_t T>
+template <uint32_t T, int S>
 __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, int L) {
   constexpr int kThreads = kDnThreads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
@@ -419,6 +418,9 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
     return a.h + (uint64_t) (t * K + blk / nblk) * a.ff + (blk % nblk) * 32 + i;
   };
   const uint32_t hblocks = K * nblk;
+  // the picks' expert ids first: the weights wait on them, and loads are waited for in issue order
+  const int32_t pid = threadIdx.x < K ? a.ids[t * K + threadIdx.x] : 0;
+  __builtin_amdgcn_sched_barrier(0);
   Rounded rh;
   round_load<kThreads>(rh, hval, hblocks, 0);
   const uint64_t o = (uint64_t) t * a.dim + r0 + threadIdx.x;
@@ -426,7 +428,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   GridStage<T, kThreads, false> gs;  // (the full table: expanding it in 4 of the 16 waves is slower here)
   grid_load(gs);
   int32_t* picks = (int32_t*) (smem + L_.picks);  // [j]: pick j's expert; [kMaxK + r]: the pick j of rank r
-  if (threadIdx.x < K) picks[threadIdx.x] = a.ids[t * K + threadIdx.x];
+  if (threadIdx.x < K) picks[threadIdx.x] = pid;
   __syncthreads();
   int8_t* q = (int8_t*) (smem + L_.q);
   float* d = (float*) (smem + L_.d);
@@ -437,7 +439,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   auto wsrc = [=](uint32_t j) __attribute__((always_inline)) { return down + (uint64_t) picks[j] * db; };
   {
     Staged st;
-    stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, 0);
+    stage_load<kThreads, S>(st, wsrc, nw, per_seg, inv_seg, 0);
     if (threadIdx.x < kWave) {  // wave 0, a lane a pick: its rank in ascending expert id (then pick); and its h
       const uint32_t j = threadIdx.x;
       const int32_t ex = j < K ? picks[j] : INT32_MAX;
@@ -450,10 +452,10 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
     }
     grid_store(gs, smem + L_.grid);
     round_store<kThreads>(rh, hblocks, 0, nblk, a.ff, q, d);
-    stage_store<kThreads>(st, smem + L_.w, nw, 0);
-    for (uint32_t base = kPer * kThreads; base < nw; base += kPer * kThreads) {
-      stage_load<kThreads>(st, wsrc, nw, per_seg, inv_seg, base);
-      stage_store<kThreads>(st, smem + L_.w, nw, base);
+    stage_store<kThreads, S>(st, smem + L_.w, nw, 0);
+    for (uint32_t base = S * kThreads; base < nw; base += S * kThreads) {
+      stage_load<kThreads, S>(st, wsrc, nw, per_seg, inv_seg, base);
+      stage_store<kThreads, S>(st, smem + L_.w, nw, base);
     }
     for (uint32_t base = kRoundBlocks<kThreads>; base < hblocks; base += kRoundBlocks<kThreads>) {
       round_load<kThreads>(rh, hval, hblocks, base);
@@ -462,28 +464,22 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   }
   __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
-  float* subs = (float*) (smem + L_.subs);  // [j 8 + row][s]
-  float* ye = (float*) (smem + L_.ye);      // [j 8 + row]
-  // phase A: (pick, block, row) items, the row fastest: 8 lanes share one pick's block of x
-  const uint32_t items = K * kDnRows * nblk;
-  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
-    const uint32_t row = it % kDnRows, js = it / kDnRows, j = js / nblk, s = js % nblk;
-    Codes c;
-    codes<T>(smem + L_.w + (j * kDnRows + row) * rb + (s / per) * bb, (int) (s % per), c, grid);
-    int x[8];
-    const int4* xp = (const int4*) (q + j * a.ff + s * 32);
-    const int4 x0 = xp[0], x1 = xp[1];
-    x[0] = x0.x, x[1] = x0.y, x[2] = x0.z, x[3] = x0.w, x[4] = x1.x, x[5] = x1.y, x[6] = x1.z, x[7] = x1.w;
-    subs[(j * kDnRows + row) * (nblk + 1) + s] = block_sum<T>(c, x);
-  }
-  __syncthreads();
-  // phase B: a chain a (pick, row, logical lane)
+  float* ye = (float*) (smem + L_.ye);  // [j 8 + row]
+  // phases A and B as one: a thread a chain (pick j, row, logical lane ll), the lane fastest, then the row (a wave's
+  // rows share their blocks of x): the lane's blocks s = ll, ll + L, ... each summed (block_sum) and chained in order,
+  // acc = fmaf(d[s], sub, acc), then the tree across the row's L lanes
   const uint32_t chains = K * kDnRows * L, lgL = L == 32 ? 5 : 4;
   for (uint32_t ch = threadIdx.x; ch < (chains + kWave - 1) / kWave * kWave; ch += kThreads) {
     const uint32_t ll = ch & (L - 1), unit = (ch >> lgL) < K * kDnRows ? ch >> lgL : 0, j = unit / kDnRows;
-    const float* sb = subs + unit * (nblk + 1);
+    const uint8_t* wr = smem + L_.w + unit * rb;
     float acc = 0.0f;
-    for (uint32_t s = ll; s < nblk; s += L) acc = __builtin_fmaf(d[j * nblk + s], sb[s], acc);
+    for (uint32_t s = ll; s < nblk; s += L) {
+      Codes c;
+      codes<T>(wr + (s / per) * bb, (int) (s % per), c, grid);
+      int x[8];
+      load_x(q, j * a.ff + s * 32, x);
+      acc = __builtin_fmaf(d[j * nblk + s], block_sum<T>(c, x), acc);
+    }
     const float v = tree_rt(acc, L);
     if (ll == 0 && ch < chains) ye[unit] = v;
   }
@@ -509,7 +505,7 @@ __global__ __launch_bounds__(GuShape<NT>::threads) void gu_kernel(GuArgs a) {
 // lane_swiglu(gate, up, lim, w[m]) into h[m][row].
 constexpr int kG1Threads = GuShape<1>::threads;
 constexpr uint32_t kG1Rows = GuShape<1>::rows;
-constexpr uint32_t kG1Slots = kPer / 2;  // staging slots a matrix: its rows at most kG1Slots kG1Threads words
+constexpr uint32_t kG1Slots = kPer / 2;  // staging slots a matrix at most: its rows at most kG1Slots kG1Threads words
 
 // gu1_kernel's LDS: the codebook first (its lookups need no base), x's codes and scales, the gate and up rows, sums
 struct G1Lds {
@@ -527,7 +523,8 @@ __host__ __device__ inline G1Lds g1_lds(uint32_t row_bytes, uint32_t dim, uint32
   return l;
 }
 
-template <uint32_t T, int L>
+// S: staging slots a matrix (the fewest that hold its tile rows, at most kG1Slots)
+template <uint32_t T, int L, int S>
 __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   constexpr int kThreads = kG1Threads;
@@ -537,9 +534,9 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   const G1Lds L_ = g1_lds(rb, a.dim, grid_bytes<T>());
   const uint32_t per_seg = kG1Rows * rb / 16;  // a matrix's words
   // the lane's word of each slot (past the matrix's end: its last word again, loaded and not stored)
-  uint32_t idx[kG1Slots];
+  uint32_t idx[S];
 #pragma unroll
-  for (uint32_t u = 0; u < kG1Slots; u++) idx[u] = min(u * kThreads + threadIdx.x, per_seg - 1);
+  for (uint32_t u = 0; u < (uint32_t) S; u++) idx[u] = min(u * kThreads + threadIdx.x, per_seg - 1);
   const uint32_t e = (uint32_t) a.ids[m];  // (an expert id: not negative; unsigned, so no sign extension to wait for)
   const float wm = a.w[m];
   GridStage<T, kThreads> gs;
@@ -551,19 +548,19 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
   const u32x4* usrc = (const u32x4*) (a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb);
-  u32x4 wv[2 * kG1Slots];
+  u32x4 wv[2 * S];
 #pragma unroll
-  for (uint32_t u = 0; u < kG1Slots; u++) wv[u] = gsrc[idx[u]], wv[kG1Slots + u] = usrc[idx[u]];
+  for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = gsrc[idx[u]], wv[S + u] = usrc[idx[u]];
   int8_t* q = (int8_t*) (smem + L_.q);
   float* d = (float*) (smem + L_.d);
   grid_store(gs, smem + L_.grid);
   round_store<kThreads>(rx, nblk, 0, nblk, a.dim, q, d);
 #pragma unroll
-  for (uint32_t u = 0; u < kG1Slots; u++) {
+  for (uint32_t u = 0; u < (uint32_t) S; u++) {
     const uint32_t l = u * kThreads + threadIdx.x;
     if (l < per_seg) {
       ((u32x4*) (smem + L_.w))[l] = wv[u];
-      ((u32x4*) (smem + L_.w))[per_seg + l] = wv[kG1Slots + u];
+      ((u32x4*) (smem + L_.w))[per_seg + l] = wv[S + u];
     }
   }
   __syncthreads();
@@ -601,10 +598,11 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   }
 }
 
-template <uint32_t T, int L>
+// S: staging slots a round (1, 2 or kPer: the fewest that hold the tile in one round)
+template <uint32_t T, int L, int S>
 __global__ __launch_bounds__(kDnThreads) void dn_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  dn_item<T>(a, blockIdx.y, blockIdx.x, smem, L);
+  dn_item<T, S>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
 }  // namespace fused

@@ -38,20 +38,33 @@ bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
   const fused::G1Lds l = fused::g1_lds(rb, a.dim, fused::grid_bytes<T>());
   if (l.total > 64 * 1024) return true;
   *taken = true;
-  fused::gu1_kernel<T, L><<<dim3(a.ff / fused::kG1Rows, a.k), fused::kG1Threads, l.total, s>>>(a);
+  const dim3 grid(a.ff / fused::kG1Rows, a.k);
+  if (fused::kG1Rows * rb / 16 <= (uint32_t) fused::kG1Threads)
+    fused::gu1_kernel<T, L, 1><<<grid, fused::kG1Threads, l.total, s>>>(a);
+  else
+    fused::gu1_kernel<T, L, fused::kG1Slots><<<grid, fused::kG1Threads, l.total, s>>>(a);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <uint32_t T, int L, int S>
+bool dn_launch_s(const DnArgs& a, hipStream_t s, uint32_t lds) {
+  auto k = fused::dn_kernel<T, L, S>;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) != hipSuccess)
+    return false;
+  k<<<dim3(a.dim / fused::kDnRows, a.n_tok), fused::kDnThreads, lds, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
 template <uint32_t T, int L>
 bool dn_launch(const DnArgs& a, hipStream_t s) {
-  const fused::DnLds l = fused::dn_lds((uint32_t) row_bytes<T>(a.ff), a.ff, a.k, fused::grid_bytes<T>());
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.ff);
+  const fused::DnLds l = fused::dn_lds(rb, a.ff, a.k, fused::grid_bytes<T>());
   if (l.total > 160 * 1024) return false;
-  auto k = fused::dn_kernel<T, L>;
-  if (l.total > 64 * 1024 &&
-      hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
-    return false;
-  k<<<dim3(a.dim / fused::kDnRows, a.n_tok), fused::kDnThreads, l.total, s>>>(a);
-  return hipGetLastError() == hipSuccess;
+  const uint32_t words = a.k * fused::kDnRows * rb / 16;  // the tile's 16-byte words: slots enough for one round
+  if (words <= (uint32_t) fused::kDnThreads) return dn_launch_s<T, L, 1>(a, s, l.total);
+  if (words <= 2u * fused::kDnThreads) return dn_launch_s<T, L, 2>(a, s, l.total);
+  return dn_launch_s<T, L, fused::kPer>(a, s, l.total);
 }
 
 template <uint32_t T>
