@@ -194,6 +194,34 @@ __device__ __forceinline__ void round_store(const Rounded& r, uint32_t blocks, u
 }
 
 
+// rows of 32-value blocks rounded as q8_round rounds them (reference kernels/q8.h:263-277), 4 lanes a block (8 values
+// each: two float4): round8_load() issues the loads of blocks base .. base + NTH / 4 - 1, value(blk, c) the address of
+// block blk's value c; round8_store() takes the block's max |x| by a 2-step xor exchange among its 4 lanes (max is
+// exact in any order), writes its 32 codes at q + 32 blk and its scale d[blk]
+struct Rounded8 {
+  f32x4 a, b;
+};
+template <int NTH, typename Val>
+__device__ __forceinline__ void round8_load(Rounded8& r, Val value, uint32_t blocks, uint32_t base) {
+  const uint32_t blk = base + threadIdx.x / 4, c = 8 * (threadIdx.x % 4), b = blk < blocks ? blk : 0;
+  r.a = *(const f32x4*) value(b, c), r.b = *(const f32x4*) value(b, c + 4);
+}
+template <int NTH>
+__device__ __forceinline__ void round8_store(const Rounded8& r, uint32_t blocks, uint32_t base, int8_t* q, float* d) {
+  const uint32_t blk = base + threadIdx.x / 4, c = 8 * (threadIdx.x % 4);
+  float am = fmaxf(fmaxf(fmaxf(fabsf(r.a.x), fabsf(r.a.y)), fmaxf(fabsf(r.a.z), fabsf(r.a.w))),
+                   fmaxf(fmaxf(fabsf(r.b.x), fabsf(r.b.y)), fmaxf(fabsf(r.b.z), fabsf(r.b.w))));
+  am = fmaxf(am, xor_lane(am, 1));
+  am = fmaxf(am, xor_lane(am, 2));
+  if (blk < blocks) {
+    const float inv = am > 0.0f ? __fdiv_rn(127.0f, am) : 0.0f;
+    uint32_t* dst = (uint32_t*) (q + blk * 32 + c);
+    dst[0] = q8_byte(r.a.x, inv) | q8_byte(r.a.y, inv) << 8 | q8_byte(r.a.z, inv) << 16 | q8_byte(r.a.w, inv) << 24;
+    dst[1] = q8_byte(r.b.x, inv) | q8_byte(r.b.y, inv) << 8 | q8_byte(r.b.z, inv) << 16 | q8_byte(r.b.w, inv) << 24;
+    if (c == 0) d[blk] = __fdiv_rn(am, 127.0f);
+  }
+}
+
 // the codebook (1 - 16 KB of constant memory, 16-aligned): grid_load() issues its loads into registers, grid_store()
 // writes them to the workgroup's LDS copy - apart, so the loads can be issued first and waited for last. IQ3_XXS's
 // signed table (16 KB) is not loaded: its 256 grid words (1 KB) are, and each is expanded in LDS to its 16 sign
@@ -371,7 +399,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
     for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
       const uint32_t row = it % kGuRows, mm = (it / kGuRows) & 1, s = it / (2 * kGuRows);
       Codes c;
-      codes<T>(smem + (mm ? L_.wu : L_.wg) + row * rb + (s / per) * bb, (int) (s % per), c, grid);
+      codes<T>((lbytes) (smem + (mm ? L_.wu : L_.wg) + row * rb + (s / per) * bb), (int) (s % per), c, grid);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         int x[8];
@@ -421,8 +449,8 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   // the picks' expert ids first: the weights wait on them, and loads are waited for in issue order
   const int32_t pid = threadIdx.x < K ? a.ids[t * K + threadIdx.x] : 0;
   __builtin_amdgcn_sched_barrier(0);
-  Rounded rh;
-  round_load<kThreads>(rh, hval, hblocks, 0);
+  Rounded8 rh;
+  round8_load<kThreads>(rh, hval, hblocks, 0);
   const uint64_t o = (uint64_t) t * a.dim + r0 + threadIdx.x;
   const float addv = threadIdx.x < kDnRows ? a.add[o] : 0.0f;  // (loaded now: its latency off the tile's end)
   GridStage<T, kThreads, false> gs;  // (the full table: expanding it in 4 of the 16 waves is slower here)
@@ -451,15 +479,15 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
       if (j < K) picks[kMaxK + rank] = (int32_t) j;
     }
     grid_store(gs, smem + L_.grid);
-    round_store<kThreads>(rh, hblocks, 0, nblk, a.ff, q, d);
+    round8_store<kThreads>(rh, hblocks, 0, q, d);
     stage_store<kThreads, S>(st, smem + L_.w, nw, 0);
     for (uint32_t base = S * kThreads; base < nw; base += S * kThreads) {
       stage_load<kThreads, S>(st, wsrc, nw, per_seg, inv_seg, base);
       stage_store<kThreads, S>(st, smem + L_.w, nw, base);
     }
-    for (uint32_t base = kRoundBlocks<kThreads>; base < hblocks; base += kRoundBlocks<kThreads>) {
-      round_load<kThreads>(rh, hval, hblocks, base);
-      round_store<kThreads>(rh, hblocks, base, nblk, a.ff, q, d);
+    for (uint32_t base = kThreads / 4; base < hblocks; base += kThreads / 4) {
+      round8_load<kThreads>(rh, hval, hblocks, base);
+      round8_store<kThreads>(rh, hblocks, base, q, d);
     }
   }
   __syncthreads();
@@ -475,7 +503,7 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
     float acc = 0.0f;
     for (uint32_t s = ll; s < nblk; s += L) {
       Codes c;
-      codes<T>(wr + (s / per) * bb, (int) (s % per), c, grid);
+      codes<T>((lbytes) (wr + (s / per) * bb), (int) (s % per), c, grid);
       int x[8];
       load_x(q, j * a.ff + s * 32, x);
       acc = __builtin_fmaf(d[j * nblk + s], block_sum<T>(c, x), acc);
@@ -497,41 +525,33 @@ __global__ __launch_bounds__(GuShape<NT>::threads) void gu_kernel(GuArgs a) {
   gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
-// gu1_kernel: the one-token gate/up (decode) - gu_kernel's tile for a token alone, its loads issued with no work
-// between the expert id's arrival and the weights' issue: each 16-byte word's offset in its matrix's kG1Rows rows is
-// set before the id is waited for, the rows' bases are scalar (the id is a scalar load), and every staging slot holds
-// one matrix's words, so a slot's loads are one scalar base plus the lane's offset. workgroup (tile, pick m): rows
-// kG1Rows tile .. of the gate and up matrices of expert ids[m]; then phase A and B as gu_kernel's and
-// lane_swiglu(gate, up, lim, w[m]) into h[m][row].
+// gu1_kernel: the one-token gate/up (decode), for dim up to kG1MaxDim (16 logical lanes a row). workgroup (tile,
+// pick m): rows kG1Rows tile .. of the gate and up matrices of expert ids[m]; lane_swiglu(gate, up, lim, w[m]) into
+// h[m][row]. its loads are issued with no work between the expert id's arrival and the weights' issue: each 16-byte
+// word's offset in its matrix's rows is set before the id is waited for, the rows' bases are scalar (the id is a
+// scalar load), and every staging slot holds one matrix's words (a slot's loads: one scalar base plus the lane's
+// offset). its LDS is a static array laid out for kG1MaxDim, so every LDS address folds into the instruction.
 constexpr int kG1Threads = GuShape<1>::threads;
-constexpr uint32_t kG1Rows = GuShape<1>::rows;
+constexpr uint32_t kG1Rows = GuShape<1>::rows, kG1MaxDim = 2048;
 constexpr uint32_t kG1Slots = kPer / 2;  // staging slots a matrix at most: its rows at most kG1Slots kG1Threads words
+static_assert(kG1Threads == (int) kG1Rows * kWave, "gu1_kernel: a wave a row");
 
-// gu1_kernel's LDS: the codebook first (its lookups need no base), x's codes and scales, the gate and up rows, sums
+// gu1_kernel's LDS: the codebook first, x's codes and scales, the gate and up rows
+template <uint32_t T>
 struct G1Lds {
-  uint32_t grid, q, d, w, subs, total;
+  static constexpr uint32_t grid = 0, q = align16(grid_bytes<T>()), d = q + kG1MaxDim, w = d + kG1MaxDim / 32 * 4;
+  static constexpr uint32_t total = w + align16(2 * kG1Rows * (uint32_t) row_bytes<T>(kG1MaxDim));
 };
-__host__ __device__ inline G1Lds g1_lds(uint32_t row_bytes, uint32_t dim, uint32_t grid_bytes) {
-  G1Lds l;
-  uint32_t at = 0;
-  l.grid = at, at += align16(grid_bytes);
-  l.q = at, at += align16(dim);
-  l.d = at, at += align16((dim / 32) * 4);
-  l.w = at, at += align16(2 * kG1Rows * row_bytes);
-  l.subs = at, at += align16(2 * kG1Rows * (dim / 32 + 1) * 4);
-  l.total = at;
-  return l;
-}
 
 // S: staging slots a matrix (the fewest that hold its tile rows, at most kG1Slots)
-template <uint32_t T, int L, int S>
+template <uint32_t T, int S>
 __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  using LD = G1Lds<T>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
   constexpr int kThreads = kG1Threads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t m = blockIdx.y, r0 = blockIdx.x * kG1Rows;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
-  const G1Lds L_ = g1_lds(rb, a.dim, grid_bytes<T>());
   const uint32_t per_seg = kG1Rows * rb / 16;  // a matrix's words
   // the lane's word of each slot (past the matrix's end: its last word again, loaded and not stored)
   uint32_t idx[S];
@@ -541,9 +561,9 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   const float wm = a.w[m];
   GridStage<T, kThreads> gs;
   grid_load(gs);
-  Rounded rx;  // (the one token's row)
-  round_load<kThreads>(rx, [=](uint32_t blk, uint32_t i) __attribute__((always_inline)) { return a.x + blk * 32 + i; },
-                       nblk, 0);
+  Rounded8 rx;  // (the one token's row: its blocks fit one round)
+  round8_load<kThreads>(rx, [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return a.x + blk * 32 + c; },
+                        nblk, 0);
   // (a scheduling barrier: the codebook and x loads issue before the id is waited for)
   __builtin_amdgcn_sched_barrier(0);
   const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
@@ -551,51 +571,51 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   u32x4 wv[2 * S];
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = gsrc[idx[u]], wv[S + u] = usrc[idx[u]];
-  int8_t* q = (int8_t*) (smem + L_.q);
-  float* d = (float*) (smem + L_.d);
-  grid_store(gs, smem + L_.grid);
-  round_store<kThreads>(rx, nblk, 0, nblk, a.dim, q, d);
+  int8_t* q = (int8_t*) (smem + LD::q);
+  float* d = (float*) (smem + LD::d);
+  grid_store(gs, smem + LD::grid);
+  round8_store<kThreads>(rx, nblk, 0, q, d);
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) {
     const uint32_t l = u * kThreads + threadIdx.x;
     if (l < per_seg) {
-      ((u32x4*) (smem + L_.w))[l] = wv[u];
-      ((u32x4*) (smem + L_.w))[per_seg + l] = wv[S + u];
+      ((u32x4*) (smem + LD::w))[l] = wv[u];
+      ((u32x4*) (smem + LD::w))[per_seg + l] = wv[S + u];
     }
   }
   __syncthreads();
-  const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
-  float* subs = (float*) (smem + L_.subs);  // [unit][s], unit = kG1Rows matrix + row
-  // phase A: (block, unit) items, the unit fastest: the units of a block share its x
-  constexpr uint32_t U = 2 * kG1Rows;
-  const uint32_t items = U * nblk;
-  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
-    const uint32_t unit = it % U, sb = it / U;
-    Codes c;
-    codes<T>(smem + L_.w + unit * rb + (sb / per) * bb, (int) (sb % per), c, grid);
-    int x[8];
-    load_x(q, sb * 32, x);
-    subs[unit * (nblk + 1) + sb] = block_sum<T>(c, x);
-  }
-  __syncthreads();
-  // phase B, in wave 0 alone (no more barriers): lane l is logical lane l % L of rows l / L + (64 / L) i; for each,
-  // the gate and up chains and trees, then lane_swiglu from the group's first lane
-  if (threadIdx.x < kWave) {
-    const uint32_t ll = threadIdx.x % L;
+  const auto* grid = (const typename GridOf<T>::E*) (smem + LD::grid);
+  // one wave a row (wave w: row w), its gate chains in lanes 0 .. 31 and its up chains in 32 .. 63; logical lane
+  // ll = l % 16's chain, blocks s = ll + 16 i for i < C = nblk / 16, is split in two: lanes 0 .. 15 (of each half)
+  // take i < CA = (C + 1) / 2, lanes 16 .. 31 the rest. every lane sums its blocks (block_sum); the first lanes run
+  // the chain's first links, acc = fmaf(d[s], sub, acc) from 0, and hand acc to lane l + 16 (xor 16), which runs the
+  // rest; then the tree over lanes 16 .. 31 - the contract's links in its order, with no barrier and no sums in LDS
+  const uint32_t lane = threadIdx.x % kWave, row = threadIdx.x / kWave, half = lane / 16 % 2, ll = lane % 16;
+  const uint32_t C = nblk / 16, CA = (C + 1) / 2, i0 = half ? CA : 0, n_i = half ? C - CA : CA;
+  const uint8_t* wr = smem + LD::w + ((lane / 32) * kG1Rows + row) * rb;
+  float sub[2] = {0.0f, 0.0f}, xd[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (uint32_t i = 0; i < kG1Rows * L / kWave; i++) {
-      const uint32_t row = threadIdx.x / L + (kWave / L) * i;
-      const float* sg = subs + row * (nblk + 1);
-      const float* su = subs + (kG1Rows + row) * (nblk + 1);
-      float ag = 0.0f, au = 0.0f;
-      for (uint32_t s = ll; s < nblk; s += L) {
-        const float xd = d[s];
-        ag = __builtin_fmaf(xd, sg[s], ag), au = __builtin_fmaf(xd, su[s], au);
-      }
-      const float g = tree<L>(ag), u = tree<L>(au);
-      if (ll == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);
+  for (uint32_t k = 0; k < 2; k++)
+    if (k < n_i) {
+      const uint32_t sb = ll + 16 * (i0 + k);
+      Codes c;
+      codes<T>((lbytes) (wr + (sb / per) * bb), (int) (sb % per), c, grid);
+      int x[8];
+      load_x(q, sb * 32, x);
+      sub[k] = block_sum<T>(c, x), xd[k] = d[sb];
     }
-  }
+  float acc = 0.0f;  // the first lanes' links
+#pragma unroll
+  for (uint32_t k = 0; k < 2; k++)
+    if (k < CA) acc = __builtin_fmaf(xd[k], sub[k], acc);
+  acc = xor_lane(acc, 16);  // (the second lanes now hold their first lanes' acc)
+#pragma unroll
+  for (uint32_t k = 0; k < 2; k++)
+    if (k < C - CA) acc = __builtin_fmaf(xd[k], sub[k], acc);
+  const float v = tree<16>(acc);
+  const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  if (lane == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);
 }
 
 // S: staging slots a round (1, 2 or kPer: the fewest that hold the tile in one round)

@@ -87,23 +87,34 @@ template <uint32_t T> __device__ inline const typename GridOf<T>::E* const_grid(
   else return nullptr;
 }
 
-template <uint32_t T> __device__ void codes(const uint8_t* b, int j, Codes& c, const typename GridOf<T>::E* grid);
+// the block bytes' readers: from generic (global) memory, or from LDS (lbytes: an LDS address). a 2-aligned address's
+// 16-bit words are read one at a time in LDS (ld16s: volatile, so the compiler does not merge neighbours into one
+// wider read, which LDS serves slowly when the address is not aligned to its width); elsewhere plain reads
+typedef const __attribute__((address_space(3))) uint8_t* lbytes;
+typedef const __attribute__((address_space(3))) volatile uint16_t* lds16v;
+using osm::ld16;
+__device__ inline uint32_t ld16(lbytes p) { return *(const __attribute__((address_space(3))) uint16_t*) p; }
+__device__ inline uint32_t ld16s(const uint8_t* p) { return ld16(p); }
+__device__ inline uint32_t ld16s(lbytes p) { return *(lds16v) p; }
+template <typename B> __device__ inline uint32_t ld32s(B p) { return ld16s(p) | ld16s(p + 2) << 16; }
+template <typename B> __device__ inline uint32_t ld32b(B p) { return ld16(p) | ld16(p + 2) << 16; }
 
 // reference kernels/q8.h:46-55
-template <> __device__ inline void codes<kIQ2_XXS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ2_XXS>::E* grid) {
-  const uint8_t* q = b + 2 + 8 * j;
-  const uint32_t aux = ld32(q + 4);
+template <typename B> __device__ inline void codes_kIQ2_XXS(B b, int j, Codes& c, const GridOf<kIQ2_XXS>::E* grid) {
+  const auto q = b + 2 + 8 * j;
+  const uint32_t qi = ld32s(q), aux = ld32s(q + 4);
 #pragma unroll
-  for (int k = 0; k < 4; k++) signed8(grid[q[k]], ksign((aux >> (7 * k)) & 0x7F), c.w[2 * k], c.w[2 * k + 1]);
+  for (int k = 0; k < 4; k++)
+    signed8(grid[(qi >> (8 * k)) & 0xFF], ksign((aux >> (7 * k)) & 0x7F), c.w[2 * k], c.w[2 * k + 1]);
   c.s21[0] = c.s21[1] = 2 * (int) (aux >> 28) + 1;
   c.d = f16(ld16(b));
 }
 
 // reference kernels/q8.h:57-66
-template <> __device__ inline void codes<kIQ2_XS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ2_XS>::E* grid) {
+template <typename B> __device__ inline void codes_kIQ2_XS(B b, int j, Codes& c, const GridOf<kIQ2_XS>::E* grid) {
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint32_t q = ld16(b + 2 + 2 * (4 * j + k));
+    const uint32_t q = ld16s(b + 2 + 2 * (4 * j + k));
     signed8(grid[q & 511], ksign(q >> 9), c.w[2 * k], c.w[2 * k + 1]);
   }
   const uint32_t s = b[66 + j];
@@ -112,8 +123,8 @@ template <> __device__ inline void codes<kIQ2_XS>(const uint8_t* b, int j, Codes
 }
 
 // reference kernels/q8.h:68-84
-template <> __device__ inline void codes<kIQ1_M>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ1_M>::E* grid) {
-  const uint32_t sc0 = ld32(b + 48), sc1 = ld32(b + 52);
+template <typename B> __device__ inline void codes_kIQ1_M(B b, int j, Codes& c, const GridOf<kIQ1_M>::E* grid) {
+  const uint32_t sc0 = ld32b(b + 48), sc1 = ld32b(b + 52);
   const uint64_t sc = (uint64_t) sc0 | (uint64_t) sc1 << 32;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -133,12 +144,12 @@ template <> __device__ inline void codes<kIQ1_M>(const uint8_t* b, int j, Codes&
 }
 
 // reference kernels/q8.h:86-95
-template <> __device__ inline void codes<kIQ2_S>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ2_S>::E* grid) {
+template <typename B> __device__ inline void codes_kIQ2_S(B b, int j, Codes& c, const GridOf<kIQ2_S>::E* grid) {
+  const uint32_t qi = ld32s(b + 2 + 4 * j), sg = ld32s(b + 34 + 4 * j), hi = b[66 + j];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int kk = 4 * j + k;
-    signed8(grid[b[2 + kk] | ((b[66 + j] >> (2 * k)) & 0x03) << 8], b[34 + kk], c.w[2 * k], c.w[2 * k + 1]);
-  }
+  for (int k = 0; k < 4; k++)
+    signed8(grid[((qi >> (8 * k)) & 0xFF) | ((hi >> (2 * k)) & 0x03) << 8], (sg >> (8 * k)) & 0xFF, c.w[2 * k],
+            c.w[2 * k + 1]);
   const uint32_t s = b[74 + j];
   c.s21[0] = 2 * (int) (s & 0x0F) + 1, c.s21[1] = 2 * (int) (s >> 4) + 1;
   c.d = f16(ld16(b));
@@ -147,10 +158,10 @@ template <> __device__ inline void codes<kIQ2_S>(const uint8_t* b, int j, Codes&
 // reference kernels/q8.h:97-108 (the same codes: grid entries q[2k] and q[2k + 1] signed by ksign's 8 bits - its low
 // nibble the first entry's, its top 3 bits and the 7-bit index's parity the second's), read from the signed table;
 // the four 7-bit fields' parities at once: y folds x over 8 bits, so bit 7k of y ^ (x >> 7) is field k's parity
-template <> __device__ inline void codes<kIQ3_XXS>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ3_XXS>::E* grid) {
-  const uint8_t* q = b + 2 + 8 * j;
-  const uint32_t q03 = ld16(q) | ld16(q + 2) << 16, q47 = ld16(q + 4) | ld16(q + 6) << 16;
-  const uint32_t aux = ld32(b + 66 + 4 * j);
+template <typename B> __device__ inline void codes_kIQ3_XXS(B b, int j, Codes& c, const GridOf<kIQ3_XXS>::E* grid) {
+  const auto q = b + 2 + 8 * j;
+  const uint32_t q03 = ld32s(q), q47 = ld32s(q + 4);
+  const uint32_t aux = ld32s(b + 66 + 4 * j);
   const uint32_t x = aux & 0x0FFFFFFFu;
   uint32_t y = x ^ (x >> 1);
   y ^= y >> 2;
@@ -168,22 +179,22 @@ template <> __device__ inline void codes<kIQ3_XXS>(const uint8_t* b, int j, Code
 }
 
 // reference kernels/q8.h:110-118
-template <> __device__ inline void codes<kQ2_K>(const uint8_t* b, int j, Codes& c, const GridOf<kQ2_K>::E* grid) {
-  const uint8_t* qs = b + 16 + 32 * (j / 4);
+template <typename B> __device__ inline void codes_kQ2_K(B b, int j, Codes& c, const GridOf<kQ2_K>::E* grid) {
+  const auto qs = b + 16 + 32 * (j / 4);
   const int shift = 2 * (j % 4);
 #pragma unroll
-  for (int t = 0; t < 8; t++) c.w[t] = (int) ((ld32(qs + 4 * t) >> shift) & 0x03030303u);
+  for (int t = 0; t < 8; t++) c.w[t] = (int) ((ld32b(qs + 4 * t) >> shift) & 0x03030303u);
 #pragma unroll
   for (int h = 0; h < 2; h++) c.s21[h] = 8 * (b[2 * j + h] & 0x0F), c.m8[h] = 8 * (b[2 * j + h] >> 4);
   c.d = f16(ld16(b + 80)), c.dmin = f16(ld16(b + 82));
 }
 
 // reference kernels/q8.h:120-130
-template <> __device__ inline void codes<kIQ1_S>(const uint8_t* b, int j, Codes& c, const GridOf<kIQ1_S>::E* grid) {
-  const uint32_t h = ld16(b + 34 + 2 * j);
+template <typename B> __device__ inline void codes_kIQ1_S(B b, int j, Codes& c, const GridOf<kIQ1_S>::E* grid) {
+  const uint32_t h = ld16(b + 34 + 2 * j), qi = ld32s(b + 2 + 4 * j);
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint64_t g = grid[b[2 + 4 * j + k] | ((h >> (3 * k)) & 0x07) << 8];
+    const uint64_t g = grid[((qi >> (8 * k)) & 0xFF) | ((h >> (3 * k)) & 0x07) << 8];
     c.w[2 * k] = (int) (uint32_t) g, c.w[2 * k + 1] = (int) (uint32_t) (g >> 32);
     c.delta[k] = h & 0x8000 ? -1 : 1;
   }
@@ -193,10 +204,10 @@ template <> __device__ inline void codes<kIQ1_S>(const uint8_t* b, int j, Codes&
 
 // build-defined: ggml's Q4_0 (32 values: f16 d, 16 bytes of nibbles; value i < 16 byte i's low nibble, 16 + i its
 // high), codes q - 8 (the 8 through `bias`), one part over the 32 with s21 8 - so d * isum exactly
-template <> __device__ inline void codes<kQ4_0>(const uint8_t* b, int, Codes& c, const GridOf<kQ4_0>::E* grid) {
+template <typename B> __device__ inline void codes_kQ4_0(B b, int, Codes& c, const GridOf<kQ4_0>::E* grid) {
 #pragma unroll
   for (int t = 0; t < 4; t++) {
-    const uint32_t v = ld32(b + 2 + 4 * t);
+    const uint32_t v = ld32s(b + 2 + 4 * t);
     c.w[t] = (int) (v & 0x0F0F0F0Fu), c.w[4 + t] = (int) ((v >> 4) & 0x0F0F0F0Fu);
   }
   c.s21[0] = c.s21[1] = 8;
@@ -205,30 +216,30 @@ template <> __device__ inline void codes<kQ4_0>(const uint8_t* b, int, Codes& c,
 
 // build-defined: Q4_K's group j (its 6-bit sc and m, reference kernels/quant.h:89-103's layout), codes q, one part
 // with its minimum: ((d * 8 sc) / 8) * isum - ((dmin * 8 m) / 8) * xsum
-template <> __device__ inline void codes<kQ4_K>(const uint8_t* b, int j, Codes& c, const GridOf<kQ4_K>::E* grid) {
-  const uint8_t* s = b + 4;
+template <typename B> __device__ inline void codes_kQ4_K(B b, int j, Codes& c, const GridOf<kQ4_K>::E* grid) {
+  const auto s = b + 4;
   const int sc = j < 4 ? s[j] & 0x3F : (s[j + 4] & 0x0F) | ((s[j - 4] >> 2) & 0x30);
   const int m = j < 4 ? s[j + 4] & 0x3F : (s[j + 4] >> 4) | ((s[j] >> 2) & 0x30);
-  const uint8_t* qs = b + 16 + (j / 2) * 32;
+  const auto qs = b + 16 + (j / 2) * 32;
   const int sh = 4 * (j % 2);
 #pragma unroll
-  for (int t = 0; t < 8; t++) c.w[t] = (int) ((ld32(qs + 4 * t) >> sh) & 0x0F0F0F0Fu);
+  for (int t = 0; t < 8; t++) c.w[t] = (int) ((ld32b(qs + 4 * t) >> sh) & 0x0F0F0F0Fu);
   c.s21[0] = c.s21[1] = 8 * sc, c.m8[0] = c.m8[1] = 8 * m;
   c.d = f16(ld16(b)), c.dmin = f16(ld16(b + 2));
 }
 
 // build-defined: Q3_K's values 32 j .. 32 j + 31 (reference kernels/quant.h:264-284's layout): codes q2 + 4 h - 4
 // (the 4 through `bias`), two halves, each s21 = 8 (sc - 32) of its 16-value group
-template <> __device__ inline void codes<kQ3_K>(const uint8_t* b, int j, Codes& c, const GridOf<kQ3_K>::E* grid) {
+template <typename B> __device__ inline void codes_kQ3_K(B b, int j, Codes& c, const GridOf<kQ3_K>::E* grid) {
   const int n = j / 4, jj = j % 4;
-  const uint8_t* qs = b + 32 + 32 * n;
+  const auto qs = b + 32 + 32 * n;
 #pragma unroll
   for (int t = 0; t < 8; t++) {
-    const uint32_t q2 = (ld32(qs + 4 * t) >> (2 * jj)) & 0x03030303u;
-    const uint32_t hb = (ld32(b + 4 * t) >> (4 * n + jj)) & 0x01010101u;
+    const uint32_t q2 = (ld32b(qs + 4 * t) >> (2 * jj)) & 0x03030303u;
+    const uint32_t hb = (ld32b(b + 4 * t) >> (4 * n + jj)) & 0x01010101u;
     c.w[t] = (int) (q2 + (hb << 2));
   }
-  const uint8_t* sc = b + 96;
+  const auto sc = b + 96;
 #pragma unroll
   for (int h = 0; h < 2; h++) {
     const int g = 2 * j + h, grp = g / 4, w = g % 4;
@@ -237,6 +248,20 @@ template <> __device__ inline void codes<kQ3_K>(const uint8_t* b, int j, Codes& 
     c.s21[h] = 8 * (sc6 - 32);
   }
   c.d = f16(ld16(b + 108));
+}
+
+template <uint32_t T, typename B>
+__device__ __forceinline__ void codes(B b, int j, Codes& c, const typename GridOf<T>::E* grid) {
+  if constexpr (T == kIQ2_XXS) codes_kIQ2_XXS(b, j, c, grid);
+  else if constexpr (T == kIQ2_XS) codes_kIQ2_XS(b, j, c, grid);
+  else if constexpr (T == kIQ1_M) codes_kIQ1_M(b, j, c, grid);
+  else if constexpr (T == kIQ2_S) codes_kIQ2_S(b, j, c, grid);
+  else if constexpr (T == kIQ3_XXS) codes_kIQ3_XXS(b, j, c, grid);
+  else if constexpr (T == kQ2_K) codes_kQ2_K(b, j, c, grid);
+  else if constexpr (T == kIQ1_S) codes_kIQ1_S(b, j, c, grid);
+  else if constexpr (T == kQ4_0) codes_kQ4_0(b, j, c, grid);
+  else if constexpr (T == kQ4_K) codes_kQ4_K(b, j, c, grid);
+  else if constexpr (T == kQ3_K) codes_kQ3_K(b, j, c, grid);
 }
 
 // the block's contribution before x's scale (reference kernels/q8.h:133-162)

@@ -27,22 +27,21 @@ bool gu_launch(const GuArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess;
 }
 
-// the one-token gate/up, when a matrix's tile rows fit its staging slots (false: not taken, the caller uses gu_kernel)
-template <uint32_t T, int L>
+// the one-token gate/up, for dim a multiple of 512 up to kG1MaxDim (16 lanes a row, whole 16-block chains) whose tile
+// rows fit the staging slots (false: not taken, the caller uses gu_kernel)
+template <uint32_t T>
 bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
   *taken = false;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim);
-  if ((fused::kG1Rows * rb) % 16 || fused::kG1Rows * rb / 16 > fused::kG1Slots * fused::kG1Threads ||
-      a.dim / 32 > fused::kRoundBlocks<fused::kG1Threads> || a.ff % fused::kG1Rows)
+  if (a.dim % 512 || a.dim > fused::kG1MaxDim || (fused::kG1Rows * rb) % 16 ||
+      fused::kG1Rows * rb / 16 > fused::kG1Slots * fused::kG1Threads || a.ff % fused::kG1Rows)
     return true;
-  const fused::G1Lds l = fused::g1_lds(rb, a.dim, fused::grid_bytes<T>());
-  if (l.total > 64 * 1024) return true;
   *taken = true;
   const dim3 grid(a.ff / fused::kG1Rows, a.k);
   if (fused::kG1Rows * rb / 16 <= (uint32_t) fused::kG1Threads)
-    fused::gu1_kernel<T, L, 1><<<grid, fused::kG1Threads, l.total, s>>>(a);
+    fused::gu1_kernel<T, 1><<<grid, fused::kG1Threads, 0, s>>>(a);
   else
-    fused::gu1_kernel<T, L, fused::kG1Slots><<<grid, fused::kG1Threads, l.total, s>>>(a);
+    fused::gu1_kernel<T, fused::kG1Slots><<<grid, fused::kG1Threads, 0, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -73,7 +72,7 @@ bool gu_by(const GuArgs& a, hipStream_t s) {
   const bool wide = a.dim >= 4096;  // the contract's 32 lanes a row
   if (a.n_tok == 1) {
     bool taken = false;
-    const bool ok = wide ? gu1_launch<T, 32>(a, s, &taken) : gu1_launch<T, 16>(a, s, &taken);
+    const bool ok = gu1_launch<T>(a, s, &taken);
     if (taken) return ok;
     return wide ? gu_launch<T, 1, 32>(a, s) : gu_launch<T, 1, 16>(a, s);
   }
