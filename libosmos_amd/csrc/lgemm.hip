@@ -29,14 +29,15 @@ constexpr uint32_t kTile = 16;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// (the block bytes are in LDS: lbytes, their 2-aligned words read 16 bits at a time)
 // a lane's chunk k (values 8k .. 8k + 7) of block j of a 256-value super-block: two words of int8 codes (IQ1: 8 grid +
 // delta), as codes<T> (lanedec.h) gives them for that chunk
 template <uint32_t T>
-__device__ inline void chunk(const uint8_t* b, int j, int k, const typename GridOf<T>::E* grid, uint32_t& w0,
+__device__ inline void chunk(lbytes b, int j, int k, const typename GridOf<T>::E* grid, uint32_t& w0,
                              uint32_t& w1);
 // the block's scale and each half's s21
 template <uint32_t T>
-__device__ inline void scales(const uint8_t* b, int j, float& d, int& s0, int& s1);
+__device__ inline void scales(lbytes b, int j, float& d, int& s0, int& s1);
 
 // 8 v + delta a byte, v in {-1, 0, 1} (0xFF, 0, 1): a byte permute from a pool of the three results
 __device__ inline uint32_t iq1_codes(uint32_t w, int delta) {
@@ -47,21 +48,21 @@ __device__ inline uint32_t iq1_codes(uint32_t w, int delta) {
 
 // reference kernels/q8.h:46-55
 template <>
-__device__ inline void chunk<kIQ2_XXS>(const uint8_t* b, int j, int k, const GridOf<kIQ2_XXS>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ2_XXS>(lbytes b, int j, int k, const GridOf<kIQ2_XXS>::E* grid, uint32_t& w0,
                                        uint32_t& w1) {
-  const uint8_t* q = b + 2 + 8 * j;
+  const auto q = b + 2 + 8 * j;
   int lo, hi;
-  signed8(grid[q[k]], ksign((ld32(q + 4) >> (7 * k)) & 0x7F), lo, hi);
+  signed8(grid[q[k]], ksign((ld32s(q + 4) >> (7 * k)) & 0x7F), lo, hi);
   w0 = (uint32_t) lo, w1 = (uint32_t) hi;
 }
 template <>
-__device__ inline void scales<kIQ2_XXS>(const uint8_t* b, int j, float& d, int& s0, int& s1) {
-  s0 = s1 = 2 * (int) (ld32(b + 2 + 8 * j + 4) >> 28) + 1;
+__device__ inline void scales<kIQ2_XXS>(lbytes b, int j, float& d, int& s0, int& s1) {
+  s0 = s1 = 2 * (int) (ld32s(b + 2 + 8 * j + 4) >> 28) + 1;
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:57-66
 template <>
-__device__ inline void chunk<kIQ2_XS>(const uint8_t* b, int j, int k, const GridOf<kIQ2_XS>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ2_XS>(lbytes b, int j, int k, const GridOf<kIQ2_XS>::E* grid, uint32_t& w0,
                                       uint32_t& w1) {
   const uint32_t q = ld16(b + 2 + 2 * (4 * j + k));
   int lo, hi;
@@ -69,14 +70,14 @@ __device__ inline void chunk<kIQ2_XS>(const uint8_t* b, int j, int k, const Grid
   w0 = (uint32_t) lo, w1 = (uint32_t) hi;
 }
 template <>
-__device__ inline void scales<kIQ2_XS>(const uint8_t* b, int j, float& d, int& s0, int& s1) {
+__device__ inline void scales<kIQ2_XS>(lbytes b, int j, float& d, int& s0, int& s1) {
   const uint32_t s = b[66 + j];
   s0 = 2 * (int) (s & 0x0F) + 1, s1 = 2 * (int) (s >> 4) + 1;
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:86-95
 template <>
-__device__ inline void chunk<kIQ2_S>(const uint8_t* b, int j, int k, const GridOf<kIQ2_S>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ2_S>(lbytes b, int j, int k, const GridOf<kIQ2_S>::E* grid, uint32_t& w0,
                                      uint32_t& w1) {
   const int kk = 4 * j + k;
   int lo, hi;
@@ -84,28 +85,28 @@ __device__ inline void chunk<kIQ2_S>(const uint8_t* b, int j, int k, const GridO
   w0 = (uint32_t) lo, w1 = (uint32_t) hi;
 }
 template <>
-__device__ inline void scales<kIQ2_S>(const uint8_t* b, int j, float& d, int& s0, int& s1) {
+__device__ inline void scales<kIQ2_S>(lbytes b, int j, float& d, int& s0, int& s1) {
   const uint32_t s = b[74 + j];
   s0 = 2 * (int) (s & 0x0F) + 1, s1 = 2 * (int) (s >> 4) + 1;
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:97-108, through the signed table (lanedec.h)
 template <>
-__device__ inline void chunk<kIQ3_XXS>(const uint8_t* b, int j, int k, const GridOf<kIQ3_XXS>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ3_XXS>(lbytes b, int j, int k, const GridOf<kIQ3_XXS>::E* grid, uint32_t& w0,
                                        uint32_t& w1) {
-  const uint8_t* q = b + 2 + 8 * j;
-  const uint32_t sg = (ld32(b + 66 + 4 * j) >> (7 * k)) & 0x7F, par = __builtin_popcount(sg) & 1u;
+  const auto q = b + 2 + 8 * j;
+  const uint32_t sg = (ld32s(b + 66 + 4 * j) >> (7 * k)) & 0x7F, par = __builtin_popcount(sg) & 1u;
   w0 = grid[16 * q[2 * k] + (sg & 15)];
   w1 = grid[16 * q[2 * k + 1] + ((sg >> 4) | par << 3)];
 }
 template <>
-__device__ inline void scales<kIQ3_XXS>(const uint8_t* b, int j, float& d, int& s0, int& s1) {
-  s0 = s1 = 2 * (2 * (int) (ld32(b + 66 + 4 * j) >> 28) + 1);
+__device__ inline void scales<kIQ3_XXS>(lbytes b, int j, float& d, int& s0, int& s1) {
+  s0 = s1 = 2 * (2 * (int) (ld32s(b + 66 + 4 * j) >> 28) + 1);
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:120-130
 template <>
-__device__ inline void chunk<kIQ1_S>(const uint8_t* b, int j, int k, const GridOf<kIQ1_S>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ1_S>(lbytes b, int j, int k, const GridOf<kIQ1_S>::E* grid, uint32_t& w0,
                                      uint32_t& w1) {
   const uint32_t h = ld16(b + 34 + 2 * j);
   const uint64_t g = grid[b[2 + 4 * j + k] | ((h >> (3 * k)) & 0x07) << 8];
@@ -113,13 +114,13 @@ __device__ inline void chunk<kIQ1_S>(const uint8_t* b, int j, int k, const GridO
   w0 = iq1_codes((uint32_t) g, delta), w1 = iq1_codes((uint32_t) (g >> 32), delta);
 }
 template <>
-__device__ inline void scales<kIQ1_S>(const uint8_t* b, int j, float& d, int& s0, int& s1) {
+__device__ inline void scales<kIQ1_S>(lbytes b, int j, float& d, int& s0, int& s1) {
   s0 = s1 = 2 * (int) ((ld16(b + 34 + 2 * j) >> 12) & 0x07) + 1;
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:68-84
 template <>
-__device__ inline void chunk<kIQ1_M>(const uint8_t* b, int j, int k, const GridOf<kIQ1_M>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ1_M>(lbytes b, int j, int k, const GridOf<kIQ1_M>::E* grid, uint32_t& w0,
                                      uint32_t& w1) {
   const int kk = 4 * j + k;
   const uint32_t h = (b[32 + kk / 2] >> (4 * (kk % 2))) & 0x0F;
@@ -128,8 +129,8 @@ __device__ inline void chunk<kIQ1_M>(const uint8_t* b, int j, int k, const GridO
   w0 = iq1_codes((uint32_t) g, delta), w1 = iq1_codes((uint32_t) (g >> 32), delta);
 }
 template <>
-__device__ inline void scales<kIQ1_M>(const uint8_t* b, int j, float& d, int& s0, int& s1) {
-  const uint32_t sc0 = ld32(b + 48), sc1 = ld32(b + 52);
+__device__ inline void scales<kIQ1_M>(lbytes b, int j, float& d, int& s0, int& s1) {
+  const uint32_t sc0 = ld32s(b + 48), sc1 = ld32s(b + 52);
   const uint64_t sc = (uint64_t) sc0 | (uint64_t) sc1 << 32;
   const int k0 = 4 * j, k1 = 4 * j + 2;
   s0 = 2 * (int) ((sc >> (16 * (k0 / 8) + 3 * ((k0 / 2) % 4))) & 0x07) + 1;
@@ -232,13 +233,13 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
         const uint8_t* blk = arow + (s / per) * Block<T>::bytes;
         const int j = (int) (s % per);
         uint32_t w0, w1;
-        chunk<T>(blk, j, quad, grid, w0, w1);
+        chunk<T>((lbytes) blk, j, quad, grid, w0, w1);
         const long a = (long) (((uint64_t) w1 << 32) | w0);
         const long a0 = quad < 2 ? a : 0, a1 = quad < 2 ? 0 : a;  // the first half's lanes, the second's
         if (quad == 0) {  // lanes 0 .. 15: row col's ((d s21) / 8) per half (lane_part's first two products)
           float dd;
           int s0_, s1_;
-          scales<T>(blk, j, dd, s0_, s1_);
+          scales<T>((lbytes) blk, j, dd, s0_, s1_);
           scl[col] = __fmul_rn(__fmul_rn(dd, (float) s0_), 0.125f);
           scl[kTile + col] = __fmul_rn(__fmul_rn(dd, (float) s1_), 0.125f);
         }
