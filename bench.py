@@ -476,9 +476,9 @@ def main():
                    "pct_hbm_peak": round(100 * lay["gbs"] / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(ker["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ker["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "osm::fused::gu1_kernel<IQ3_XXS,16>", "us_per_launch": round(ker["us"], 3),
+                     "kernel": "osm::fused::gu1_kernel<IQ3_XXS,1>", "us_per_launch": round(ker["us"], 3),
                      "bytes_per_launch": int(ker["bytes"])},
-        "kernels": {"osm::fused::dn_kernel<IQ3_XXS,16>": {"us_per_launch": round(dn["us"], 3),
+        "kernels": {"osm::fused::dn_kernel<IQ3_XXS,16,1>": {"us_per_launch": round(dn["us"], 3),
                                                           "bytes_per_launch": int(dn["bytes"]),
                                                           "GB/s": round(dn["gbs"], 2)}},
     }
