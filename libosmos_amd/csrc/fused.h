@@ -233,10 +233,11 @@ struct GridStage {
   static constexpr bool expand = Expand && T == kIQ3_XXS;
   static constexpr uint32_t n = expand ? 256 : grid_bytes<T>() / 16, words = expand ? 1 : 4;
   static constexpr uint32_t per = (n + NTH - 1) / NTH;
-  // expanding, a thread takes grid word (u NTH + threadIdx.x) % 256 and `quads` of its 4 groups of 4 variants
-  static constexpr uint32_t quads = NTH >= 1024 ? 1 : 1024 / NTH;
+  // expanding: the table's 1024 16-byte words (4 a grid word: its variants 4 q .. 4 q + 3) written in `passes` rounds,
+  // word p NTH + threadIdx.x in round p - consecutive lanes, consecutive words (no LDS bank conflicts)
+  static constexpr uint32_t passes = 1024 / NTH;
   static_assert(!expand || NTH >= 256 && NTH <= 1024 && NTH % 256 == 0, "the expansion's thread split");
-  uint32_t v[per > 0 ? per * words : 1];
+  uint32_t v[expand ? passes : (per > 0 ? per * words : 1)];
 };
 typedef const __attribute__((address_space(1))) uint32_t* gptr32;
 typedef const __attribute__((address_space(1))) u32x4* gptr128;
@@ -251,7 +252,8 @@ __device__ __forceinline__ void grid_load(GridStage<T, NTH, E>& g) {
   using G = GridStage<T, NTH, E>;
   if constexpr (G::expand) {
     const gptr32 src = opaque_global<gptr32>(kGrids.iq3xxs);
-    g.v[0] = src[threadIdx.x % 256];
+#pragma unroll
+    for (uint32_t p = 0; p < G::passes; p++) g.v[p] = src[(p * NTH + threadIdx.x) / 4];
   } else if constexpr (G::n > 0) {
     const gptr128 src = opaque_global<gptr128>(const_grid<T>());
 #pragma unroll
@@ -266,18 +268,16 @@ template <uint32_t T, int NTH, bool E>
 __device__ __forceinline__ void grid_store(const GridStage<T, NTH, E>& g, uint8_t* lds) {
   using G = GridStage<T, NTH, E>;
   if constexpr (G::expand) {
-    const uint32_t pos = g.v[0], neg = ~pos + 0x01010101u;  // (bytes 4 .. 62: no borrow between bytes)
-    const uint32_t q0 = (threadIdx.x / 256) * G::quads;
-    u32x4* dst = (u32x4*) lds + 4 * (threadIdx.x % 256) + q0;
+    const uint32_t qd = threadIdx.x % 4;  // (the lane's variants 4 qd .. 4 qd + 3: bits 2 and 3 of the variant)
+    const uint32_t sh = (qd & 1) * 0x040000u + (qd >> 1) * 0x04000000u;
 #pragma unroll
-    for (uint32_t qq = 0; qq < G::quads; qq++) {
-      const uint32_t hi = (q0 + qq) * 4;  // (variants 4 (q0 + qq) .. + 3: bits 2, 3 of the variant)
-      const uint32_t sh = (hi >> 2 & 1) * 0x040000u + (hi >> 3 & 1) * 0x04000000u;
+    for (uint32_t p = 0; p < G::passes; p++) {
+      const uint32_t pos = g.v[p], neg = ~pos + 0x01010101u;  // (bytes 4 .. 62: no borrow between bytes)
       uint32_t w[4];
 #pragma unroll
       for (uint32_t i = 0; i < 4; i++)
         w[i] = __builtin_amdgcn_perm(neg, pos, 0x03020100u + (i & 1) * 0x04u + (i >> 1) * 0x0400u + sh);
-      dst[qq] = u32x4{w[0], w[1], w[2], w[3]};
+      ((u32x4*) lds)[p * NTH + threadIdx.x] = u32x4{w[0], w[1], w[2], w[3]};
     }
   } else if constexpr (G::n > 0) {
 #pragma unroll
