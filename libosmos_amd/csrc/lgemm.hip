@@ -33,8 +33,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // a lane's chunk k (values 8k .. 8k + 7) of block j of a 256-value super-block: two words of int8 codes (IQ1: 8 grid +
 // delta), as codes<T> (lanedec.h) gives them for that chunk
 template <uint32_t T>
-__device__ inline void chunk(lbytes b, int j, int k, const typename GridOf<T>::E* grid, uint32_t& w0,
-                             uint32_t& w1);
+__device__ inline void chunk(lbytes b, int j, int k, const typename GridOf<T>::E* grid, const uint64_t* sm,
+                             uint32_t& w0, uint32_t& w1);
 // the block's scale and each half's s21
 template <uint32_t T>
 __device__ inline void scales(lbytes b, int j, float& d, int& s0, int& s1);
@@ -46,14 +46,28 @@ __device__ inline uint32_t iq1_codes(uint32_t w, int delta) {
   return __builtin_amdgcn_perm(0u, pool, w & 0x03030303u);  // v's low 2 bits: 0 -> byte 0, 1 -> 1, 3 (-1) -> 3
 }
 
+// 8 unsigned grid bytes negated where the byte mask m is 0xFF: (v ^ m) + (m & 1) a byte (signed8's arithmetic, the
+// mask read from a table of the 128 7-bit sign fields' masks, parity bit included)
+__device__ inline void signs8(uint64_t g, uint64_t m, uint32_t& w0, uint32_t& w1) {
+  const uint32_t m0 = (uint32_t) m, m1 = (uint32_t) (m >> 32);
+  w0 = ((uint32_t) g ^ m0) + (m0 & 0x01010101u), w1 = ((uint32_t) (g >> 32) ^ m1) + (m1 & 0x01010101u);
+}
+// the table: entry i, ksign(i)'s 8 bits as bytes of 0xFF (set) or 0
+__device__ inline uint64_t sign_mask(uint32_t i) {
+  const uint32_t s = ksign(i);
+  uint64_t m = 0;
+#pragma unroll
+  for (int b = 0; b < 8; b++) m |= (uint64_t) ((s >> b) & 1u) * (0xFFull << (8 * b));
+  return m;
+}
+
 // reference kernels/q8.h:46-55
 template <>
-__device__ inline void chunk<kIQ2_XXS>(lbytes b, int j, int k, const GridOf<kIQ2_XXS>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ2_XXS>(lbytes b, int j, int k, const GridOf<kIQ2_XXS>::E* grid, const uint64_t* sm,
+                                       uint32_t& w0,
                                        uint32_t& w1) {
   const auto q = b + 2 + 8 * j;
-  int lo, hi;
-  signed8(grid[q[k]], ksign((ld32s(q + 4) >> (7 * k)) & 0x7F), lo, hi);
-  w0 = (uint32_t) lo, w1 = (uint32_t) hi;
+  signs8(grid[q[k]], sm[(ld32s(q + 4) >> (7 * k)) & 0x7F], w0, w1);
 }
 template <>
 __device__ inline void scales<kIQ2_XXS>(lbytes b, int j, float& d, int& s0, int& s1) {
@@ -62,12 +76,11 @@ __device__ inline void scales<kIQ2_XXS>(lbytes b, int j, float& d, int& s0, int&
 }
 // reference kernels/q8.h:57-66
 template <>
-__device__ inline void chunk<kIQ2_XS>(lbytes b, int j, int k, const GridOf<kIQ2_XS>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ2_XS>(lbytes b, int j, int k, const GridOf<kIQ2_XS>::E* grid, const uint64_t* sm,
+                                       uint32_t& w0,
                                       uint32_t& w1) {
   const uint32_t q = ld16(b + 2 + 2 * (4 * j + k));
-  int lo, hi;
-  signed8(grid[q & 511], ksign(q >> 9), lo, hi);
-  w0 = (uint32_t) lo, w1 = (uint32_t) hi;
+  signs8(grid[q & 511], sm[q >> 9], w0, w1);
 }
 template <>
 __device__ inline void scales<kIQ2_XS>(lbytes b, int j, float& d, int& s0, int& s1) {
@@ -77,7 +90,8 @@ __device__ inline void scales<kIQ2_XS>(lbytes b, int j, float& d, int& s0, int& 
 }
 // reference kernels/q8.h:86-95
 template <>
-__device__ inline void chunk<kIQ2_S>(lbytes b, int j, int k, const GridOf<kIQ2_S>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ2_S>(lbytes b, int j, int k, const GridOf<kIQ2_S>::E* grid, const uint64_t* sm,
+                                       uint32_t& w0,
                                      uint32_t& w1) {
   const int kk = 4 * j + k;
   int lo, hi;
@@ -92,7 +106,8 @@ __device__ inline void scales<kIQ2_S>(lbytes b, int j, float& d, int& s0, int& s
 }
 // reference kernels/q8.h:97-108, through the signed table (lanedec.h)
 template <>
-__device__ inline void chunk<kIQ3_XXS>(lbytes b, int j, int k, const GridOf<kIQ3_XXS>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ3_XXS>(lbytes b, int j, int k, const GridOf<kIQ3_XXS>::E* grid, const uint64_t* sm,
+                                       uint32_t& w0,
                                        uint32_t& w1) {
   const auto q = b + 2 + 8 * j;
   const uint32_t sg = (ld32s(b + 66 + 4 * j) >> (7 * k)) & 0x7F, par = __builtin_popcount(sg) & 1u;
@@ -106,7 +121,8 @@ __device__ inline void scales<kIQ3_XXS>(lbytes b, int j, float& d, int& s0, int&
 }
 // reference kernels/q8.h:120-130
 template <>
-__device__ inline void chunk<kIQ1_S>(lbytes b, int j, int k, const GridOf<kIQ1_S>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ1_S>(lbytes b, int j, int k, const GridOf<kIQ1_S>::E* grid, const uint64_t* sm,
+                                       uint32_t& w0,
                                      uint32_t& w1) {
   const uint32_t h = ld16(b + 34 + 2 * j);
   const uint64_t g = grid[b[2 + 4 * j + k] | ((h >> (3 * k)) & 0x07) << 8];
@@ -120,7 +136,8 @@ __device__ inline void scales<kIQ1_S>(lbytes b, int j, float& d, int& s0, int& s
 }
 // reference kernels/q8.h:68-84
 template <>
-__device__ inline void chunk<kIQ1_M>(lbytes b, int j, int k, const GridOf<kIQ1_M>::E* grid, uint32_t& w0,
+__device__ inline void chunk<kIQ1_M>(lbytes b, int j, int k, const GridOf<kIQ1_M>::E* grid, const uint64_t* sm,
+                                       uint32_t& w0,
                                      uint32_t& w1) {
   const int kk = 4 * j + k;
   const uint32_t h = (b[32 + kk / 2] >> (4 * (kk % 2))) & 0x0F;
@@ -146,15 +163,16 @@ constexpr uint32_t grid_bytes_of() {
   return GridOf<T>::n * sizeof(typename GridOf<T>::E);
 }
 
-// dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the waves' scale tables and their
-// partial trees
+// dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the sign masks, the waves' scale tables
+// and their partial trees
 template <uint32_t T, int CT>
 struct Lds {
-  uint32_t slab, grid, scl, part, total;
+  uint32_t slab, grid, sm, scl, part, total;
   __host__ __device__ Lds(uint32_t rb) {
     slab = 0;
     grid = (16 * rb + 15) / 16 * 16;
-    scl = grid + grid_bytes_of<T>();
+    sm = grid + grid_bytes_of<T>();
+    scl = sm + 128 * 8;
     part = scl + kWaves * 2 * kTile * 4;
     total = part + kWaves * CT * 4 * kWave * 4;
   }
@@ -185,20 +203,25 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
     constexpr uint32_t ng = grid_bytes_of<T>() / 16;
     const u32x4* gs = (const u32x4*) const_grid<T>();
     for (uint32_t i = threadIdx.x; i < ng; i += kThreads) ((u32x4*) (smem + L_.grid))[i] = gs[i];
+    if (threadIdx.x < 128) ((uint64_t*) (smem + L_.sm))[threadIdx.x] = sign_mask(threadIdx.x);
   }
   __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
+  const uint64_t* sm = (const uint64_t*) (smem + L_.sm);
   float* scl = (float*) (smem + L_.scl) + wave * 2 * kTile;  // [half][row]
   float* part = (float*) (smem + L_.part);                    // [wave][ct][i][lane]
   const uint8_t* arow = smem + L_.slab + col * rb;            // this lane's A row
   for (uint32_t c0 = 0; c0 < n; c0 += kTile * CT) {
-    const int8_t* xb[CT];
-    const float* xd[CT];
+    // (the matrix's first token row as a scalar base, each lane's token as a 32-bit offset from it: tokens under
+    // OSMOS_LANE_MAX_TOKENS, so tt cols fits)
+    const int8_t* qb = q + (uint64_t) r0 * cols;
+    const float* db = d + (uint64_t) r0 * nblk;
+    uint32_t xb[CT], xd[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {  // this lane's B token (past the count: the last, summed, never stored)
       const uint32_t t = c0 + ct * kTile + col, tt = t < n ? t : n - 1;
-      xb[ct] = q + (uint64_t) (r0 + tt) * cols + 8 * quad;
-      xd[ct] = d + (uint64_t) (r0 + tt) * nblk;
+      xb[ct] = tt * cols + 8 * quad;
+      xd[ct] = tt * nblk;
     }
     const int tiles = (int) ((n - c0 + kTile - 1) / kTile) < CT ? (int) ((n - c0 + kTile - 1) / kTile) : CT;
     float acc[C][CT][4];
@@ -215,8 +238,8 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) {
         const uint32_t sc = s < nblk ? s : 0;
-        bxn[ct] = *(const long*) (xb[ct] + (uint64_t) sc * 32);
-        xsn[ct] = xd[ct][sc];
+        bxn[ct] = *(const long*) (qb + (xb[ct] + sc * 32));
+        xsn[ct] = db[xd[ct] + sc];
       }
     };
     xload((uint32_t) wave);
@@ -233,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
         const uint8_t* blk = arow + (s / per) * Block<T>::bytes;
         const int j = (int) (s % per);
         uint32_t w0, w1;
-        chunk<T>((lbytes) blk, j, quad, grid, w0, w1);
+        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
         const long a = (long) (((uint64_t) w1 << 32) | w0);
         const long a0 = quad < 2 ? a : 0, a1 = quad < 2 ? 0 : a;  // the first half's lanes, the second's
         if (quad == 0) {  // lanes 0 .. 15: row col's ((d s21) / 8) per half (lane_part's first two products)
@@ -326,7 +349,7 @@ extern "C" OSM_API bool osmos_lane_group(uint32_t type, const void* const* w, co
                                          uint32_t n_mat, uint32_t max_cnt, uint32_t rows, uint32_t cols,
                                          const int8_t* q, const float* d, float* y, uint32_t ys, void* stream) {
   if (!w || !cnt || !xrow || !q || !d || !y || !n_mat || n_mat > 65535 || !max_cnt || max_cnt > OSMOS_LANE_MAX_TOKENS ||
-      !rows || rows % lgemm::kTile || !cols || cols % 256 || ys < rows)
+      !rows || rows % lgemm::kTile || !cols || cols % 256 || ys < rows || (uint64_t) max_cnt * cols >= (1ull << 31))
     return false;
   const hipStream_t s = (hipStream_t) stream;
   switch (type) {
