@@ -525,31 +525,37 @@ __global__ __launch_bounds__(GuShape<NT>::threads) void gu_kernel(GuArgs a) {
   gu_item<T, NT>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
-// gu1_kernel: the one-token gate/up (decode), for dim up to kG1MaxDim (16 logical lanes a row). workgroup (tile,
-// pick m): rows kG1Rows tile .. of the gate and up matrices of expert ids[m]; lane_swiglu(gate, up, lim, w[m]) into
-// h[m][row]. its loads are issued with no work between the expert id's arrival and the weights' issue: each 16-byte
-// word's offset in its matrix's rows is set before the id is waited for, the rows' bases are scalar (the id is a
-// scalar load), and every staging slot holds one matrix's words (a slot's loads: one scalar base plus the lane's
-// offset). its LDS is a static array laid out for kG1MaxDim, so every LDS address folds into the instruction.
+// gu1_kernel: the one-token gate/up (decode). workgroup (tile, pick m): rows kG1Rows tile .. of the gate and up
+// matrices of expert ids[m]; lane_swiglu(gate, up, lim, w[m]) into h[m][row]. its loads are issued with no work between
+// the expert id's arrival and the weights' issue: each 16-byte word's offset in its matrix's rows is set before the id
+// is waited for, the rows' bases are scalar (the id is a scalar load), and every staging slot holds one matrix's words
+// (a slot's loads: one scalar base plus the lane's offset). its LDS is a static array laid out for the largest dim of
+// its lane count (G1Max), so every LDS address folds into the instruction. one wave a row (wave w: row w), the gate's
+// lane chains in lanes 0 .. 31, the up's in 32 .. 63.
 constexpr int kG1Threads = GuShape<1>::threads;
-constexpr uint32_t kG1Rows = GuShape<1>::rows, kG1MaxDim = 2048;
-constexpr uint32_t kG1Slots = kPer / 2;  // staging slots a matrix at most: its rows at most kG1Slots kG1Threads words
+constexpr uint32_t kG1Rows = GuShape<1>::rows;
+constexpr uint32_t kG1Slots = kPer;  // staging slots a matrix at most: its rows at most kG1Slots kG1Threads words
 static_assert(kG1Threads == (int) kG1Rows * kWave, "gu1_kernel: a wave a row");
+// the dims each lane count takes: 16 lanes up to 2048 (whole 16-block chains: a multiple of 512), 32 lanes 4096 ..
+// 8192 (whole 32-block chains: a multiple of 1024)
+template <int L> struct G1Max { static constexpr uint32_t dim = L == 16 ? 2048 : 8192; };
 
 // gu1_kernel's LDS: the codebook first, x's codes and scales, the gate and up rows
-template <uint32_t T>
+template <uint32_t T, int L>
 struct G1Lds {
-  static constexpr uint32_t grid = 0, q = align16(grid_bytes<T>()), d = q + kG1MaxDim, w = d + kG1MaxDim / 32 * 4;
-  static constexpr uint32_t total = w + align16(2 * kG1Rows * (uint32_t) row_bytes<T>(kG1MaxDim));
+  static constexpr uint32_t D = G1Max<L>::dim;
+  static constexpr uint32_t grid = 0, q = align16(grid_bytes<T>()), d = q + D, w = d + D / 32 * 4;
+  static constexpr uint32_t total = w + align16(2 * kG1Rows * (uint32_t) row_bytes<T>(D));
 };
 
-// S: staging slots a matrix (the fewest that hold its tile rows, at most kG1Slots)
-template <uint32_t T, int S>
+// S: staging slots a matrix (the fewest that hold its tile rows); L: the contract's lanes a row (16 or 32)
+template <uint32_t T, int S, int L>
 __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
-  using LD = G1Lds<T>;
+  using LD = G1Lds<T, L>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
   constexpr int kThreads = kG1Threads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
+  constexpr int R = (int) (G1Max<L>::dim / 32 / (kThreads / 4));  // x's rounding rounds (4 lanes a block)
   const uint32_t m = blockIdx.y, r0 = blockIdx.x * kG1Rows;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
   const uint32_t per_seg = kG1Rows * rb / 16;  // a matrix's words
@@ -561,9 +567,11 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   const float wm = a.w[m];
   GridStage<T, kThreads> gs;
   grid_load(gs);
-  Rounded8 rx;  // (the one token's row: its blocks fit one round)
-  round8_load<kThreads>(rx, [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return a.x + blk * 32 + c; },
-                        nblk, 0);
+  Rounded8 rx[R];  // (the one token's row)
+  auto xval = [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return a.x + blk * 32 + c; };
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if (r == 0 || (uint32_t) r * (kThreads / 4) < nblk) round8_load<kThreads>(rx[r], xval, nblk, r * (kThreads / 4));
   // (a scheduling barrier: the codebook and x loads issue before the id is waited for)
   __builtin_amdgcn_sched_barrier(0);
   const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
@@ -574,7 +582,9 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   int8_t* q = (int8_t*) (smem + LD::q);
   float* d = (float*) (smem + LD::d);
   grid_store(gs, smem + LD::grid);
-  round8_store<kThreads>(rx, nblk, 0, q, d);
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if (r == 0 || (uint32_t) r * (kThreads / 4) < nblk) round8_store<kThreads>(rx[r], nblk, r * (kThreads / 4), q, d);
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) {
     const uint32_t l = u * kThreads + threadIdx.x;
@@ -585,34 +595,50 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   }
   __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + LD::grid);
-  // one wave a row (wave w: row w), its gate chains in lanes 0 .. 31 and its up chains in 32 .. 63; logical lane
-  // ll = l % 16's chain, blocks s = ll + 16 i for i < C = nblk / 16, is split in two: lanes 0 .. 15 (of each half)
-  // take i < CA = (C + 1) / 2, lanes 16 .. 31 the rest. every lane sums its blocks (block_sum); the first lanes run
-  // the chain's first links, acc = fmaf(d[s], sub, acc) from 0, and hand acc to lane l + 16 (xor 16), which runs the
-  // rest; then the tree over lanes 16 .. 31 - the contract's links in its order, with no barrier and no sums in LDS
-  const uint32_t lane = threadIdx.x % kWave, row = threadIdx.x / kWave, half = lane / 16 % 2, ll = lane % 16;
-  const uint32_t C = nblk / 16, CA = (C + 1) / 2, i0 = half ? CA : 0, n_i = half ? C - CA : CA;
+  const uint32_t lane = threadIdx.x % kWave, row = threadIdx.x / kWave;
   const uint8_t* wr = smem + LD::w + ((lane / 32) * kG1Rows + row) * rb;
-  float sub[2] = {0.0f, 0.0f}, xd[2] = {0.0f, 0.0f};
+  float v;
+  if constexpr (L == 16) {
+    // logical lane ll = l % 16's chain, blocks s = ll + 16 i for i < C = nblk / 16, is split in two: lanes 0 .. 15
+    // (of each half-wave) take i < CA = (C + 1) / 2, lanes 16 .. 31 the rest. every lane sums its blocks
+    // (block_sum); the first lanes run the chain's first links, acc = fmaf(d[s], sub, acc) from 0, and hand acc to
+    // lane l + 16 (xor 16), which runs the rest; then the tree over lanes 16 .. 31 - the contract's links in its
+    // order, with no barrier and no sums in LDS
+    const uint32_t half = lane / 16 % 2, ll = lane % 16;
+    const uint32_t C = nblk / 16, CA = (C + 1) / 2, i0 = half ? CA : 0, n_i = half ? C - CA : CA;
+    float sub[2] = {0.0f, 0.0f}, xd[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (uint32_t k = 0; k < 2; k++)
-    if (k < n_i) {
-      const uint32_t sb = ll + 16 * (i0 + k);
+    for (uint32_t k = 0; k < 2; k++)
+      if (k < n_i) {
+        const uint32_t sb = ll + 16 * (i0 + k);
+        Codes c;
+        codes<T>((lbytes) (wr + (sb / per) * bb), (int) (sb % per), c, grid);
+        int x[8];
+        load_x(q, sb * 32, x);
+        sub[k] = block_sum<T>(c, x), xd[k] = d[sb];
+      }
+    float acc = 0.0f;  // the first lanes' links
+#pragma unroll
+    for (uint32_t k = 0; k < 2; k++)
+      if (k < CA) acc = __builtin_fmaf(xd[k], sub[k], acc);
+    acc = xor_lane(acc, 16);  // (the second lanes now hold their first lanes' acc)
+#pragma unroll
+    for (uint32_t k = 0; k < 2; k++)
+      if (k < C - CA) acc = __builtin_fmaf(xd[k], sub[k], acc);
+    v = tree<16>(acc);
+  } else {
+    // logical lane ll = l % 32's whole chain, blocks s = ll + 32 i in order, then the tree over the half-wave
+    const uint32_t ll = lane % 32;
+    float acc = 0.0f;
+    for (uint32_t sb = ll; sb < nblk; sb += 32) {
       Codes c;
       codes<T>((lbytes) (wr + (sb / per) * bb), (int) (sb % per), c, grid);
       int x[8];
       load_x(q, sb * 32, x);
-      sub[k] = block_sum<T>(c, x), xd[k] = d[sb];
+      acc = __builtin_fmaf(d[sb], block_sum<T>(c, x), acc);
     }
-  float acc = 0.0f;  // the first lanes' links
-#pragma unroll
-  for (uint32_t k = 0; k < 2; k++)
-    if (k < CA) acc = __builtin_fmaf(xd[k], sub[k], acc);
-  acc = xor_lane(acc, 16);  // (the second lanes now hold their first lanes' acc)
-#pragma unroll
-  for (uint32_t k = 0; k < 2; k++)
-    if (k < C - CA) acc = __builtin_fmaf(xd[k], sub[k], acc);
-  const float v = tree<16>(acc);
+    v = tree<32>(acc);
+  }
   const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
   const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   if (lane == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);

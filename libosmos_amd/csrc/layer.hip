@@ -27,22 +27,38 @@ bool gu_launch(const GuArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess;
 }
 
-// the one-token gate/up, for dim a multiple of 512 up to kG1MaxDim (16 lanes a row, whole 16-block chains) whose tile
-// rows fit the staging slots (false: not taken, the caller uses gu_kernel)
+// the one-token gate/up: 16 lanes for dim a multiple of 512 up to 2048, 32 lanes for a multiple of 1024 from 4096 to
+// 8192, the tile rows in at most kG1Slots staging slots a matrix (false: not taken, the caller uses gu_kernel)
+template <uint32_t T, int L>
+bool gu1_launch_l(const GuArgs& a, hipStream_t s) {
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), words = fused::kG1Rows * rb / 16;
+  const dim3 grid(a.ff / fused::kG1Rows, a.k);
+  constexpr int kT = fused::kG1Threads;
+  if (words <= (uint32_t) kT)
+    fused::gu1_kernel<T, 1, L><<<grid, kT, 0, s>>>(a);
+  else if (words <= 2u * kT)
+    fused::gu1_kernel<T, 2, L><<<grid, kT, 0, s>>>(a);
+  else
+    fused::gu1_kernel<T, fused::kG1Slots, L><<<grid, kT, 0, s>>>(a);
+  return hipGetLastError() == hipSuccess;
+}
+
 template <uint32_t T>
 bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
   *taken = false;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim);
-  if (a.dim % 512 || a.dim > fused::kG1MaxDim || (fused::kG1Rows * rb) % 16 ||
-      fused::kG1Rows * rb / 16 > fused::kG1Slots * fused::kG1Threads || a.ff % fused::kG1Rows)
+  if ((fused::kG1Rows * rb) % 16 || fused::kG1Rows * rb / 16 > (uint32_t) (fused::kG1Slots * fused::kG1Threads) ||
+      a.ff % fused::kG1Rows)
     return true;
-  *taken = true;
-  const dim3 grid(a.ff / fused::kG1Rows, a.k);
-  if (fused::kG1Rows * rb / 16 <= (uint32_t) fused::kG1Threads)
-    fused::gu1_kernel<T, 1><<<grid, fused::kG1Threads, 0, s>>>(a);
-  else
-    fused::gu1_kernel<T, fused::kG1Slots><<<grid, fused::kG1Threads, 0, s>>>(a);
-  return hipGetLastError() == hipSuccess;
+  if (a.dim % 512 == 0 && a.dim <= fused::G1Max<16>::dim) {
+    *taken = true;
+    return gu1_launch_l<T, 16>(a, s);
+  }
+  if (a.dim % 1024 == 0 && a.dim >= 4096 && a.dim <= fused::G1Max<32>::dim) {
+    *taken = true;
+    return gu1_launch_l<T, 32>(a, s);
+  }
+  return true;
 }
 
 template <uint32_t T, int L, int S>
