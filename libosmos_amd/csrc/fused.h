@@ -644,6 +644,190 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   if (lane == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);
 }
 
+// gub_kernel: gate/up for a batch (n_tok >= 2), gu1_kernel's tile and lane layout with several tokens a pass.
+// workgroup (tile, pick m): owned by the first pick of its expert e (a later pick of e leaves at once); its tokens
+// are the picks of e (at most one a token), NB a pass: their x rows rounded into LDS, then each lane decodes its blocks
+// once and runs its chain links for every token of the pass (a chain accumulator a token), the trees, and
+// lane_swiglu(gate, up, lim, w[pick]) into h[pick][row] for each.
+template <uint32_t T, int L, int NB>
+struct GbLds {
+  static constexpr uint32_t D = G1Max<L>::dim;
+  static constexpr uint32_t grid = 0, q = align16(grid_bytes<T>()), d = q + NB * D, w = d + NB * (D / 32) * 4;
+  static constexpr uint32_t toks = w + align16(2 * kG1Rows * (uint32_t) row_bytes<T>(D));
+  static constexpr uint32_t ids = toks + align16((kMaxTok + 1) * 4);  // the routing ids of the first 2 kG1Threads picks
+  static constexpr uint32_t total = ids + 2 * kG1Threads * 4;
+};
+
+// one pass of gub_kernel: tokens toks[c0 .. c0 + live) (live <= NB), x rows from..NB-1 rounded into q/d (the rows
+// before from are there already), chains, trees and h
+template <uint32_t T, int L, int NB>
+__device__ __forceinline__ void gub_pass(const GuArgs& a, const int32_t* toks, int c0, int live, int from, int8_t* q,
+                                         float* d, const typename GridOf<T>::E* grid, const uint8_t* wr, uint32_t r0) {
+  constexpr int kThreads = kG1Threads;
+  constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
+  const uint32_t nblk = a.dim / 32, lane = threadIdx.x % kWave, row = threadIdx.x / kWave;
+  // the pass's x rows rounded (q8_round's bits): block b nblk + s is token b's block s (the rows past the live ones
+  // repeat the last: summed, never stored)
+  auto xval = [&](uint32_t blk, uint32_t c) __attribute__((always_inline)) {
+    const uint32_t b = blk / nblk, tb = (int) b < live ? b : (uint32_t) live - 1;
+    return a.x + (uint64_t) ((uint32_t) toks[c0 + (int) tb] / a.k) * a.dim + (blk % nblk) * 32 + c;
+  };
+  for (uint32_t base = from * nblk; base < NB * nblk; base += kThreads / 4) {
+    Rounded8 rx;
+    round8_load<kThreads>(rx, xval, NB * nblk, base);
+    round8_store<kThreads>(rx, NB * nblk, base, q, d);
+  }
+  __syncthreads();
+  float v[NB];
+  if constexpr (L == 16) {  // gu1_kernel's split chains, an accumulator a token
+    const uint32_t half = lane / 16 % 2, ll = lane % 16;
+    const uint32_t C = nblk / 16, CA = (C + 1) / 2, i0 = half ? CA : 0, n_i = half ? C - CA : CA;
+    float sub[2][NB], xd[2][NB];
+#pragma unroll
+    for (uint32_t k = 0; k < 2; k++)
+#pragma unroll
+      for (int b = 0; b < NB; b++) sub[k][b] = 0.0f, xd[k][b] = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 2; k++)
+      if (k < n_i) {
+        const uint32_t sb = ll + 16 * (i0 + k);
+        Codes c;
+        codes<T>((lbytes) (wr + (sb / per) * bb), (int) (sb % per), c, grid);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          int x[8];
+          load_x(q, (b * nblk + sb) * 32, x);
+          sub[k][b] = block_sum<T>(c, x), xd[k][b] = d[b * nblk + sb];
+        }
+      }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      float acc = 0.0f;
+#pragma unroll
+      for (uint32_t k = 0; k < 2; k++)
+        if (k < CA) acc = __builtin_fmaf(xd[k][b], sub[k][b], acc);
+      acc = xor_lane(acc, 16);
+#pragma unroll
+      for (uint32_t k = 0; k < 2; k++)
+        if (k < C - CA) acc = __builtin_fmaf(xd[k][b], sub[k][b], acc);
+      v[b] = tree<16>(acc);
+    }
+  } else {  // a lane's whole chain, an accumulator a token
+    const uint32_t ll = lane % 32;
+    float acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b] = 0.0f;
+    for (uint32_t sb = ll; sb < nblk; sb += 32) {
+      Codes c;
+      codes<T>((lbytes) (wr + (sb / per) * bb), (int) (sb % per), c, grid);
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        int x[8];
+        load_x(q, (b * nblk + sb) * 32, x);
+        acc[b] = __builtin_fmaf(d[b * nblk + sb], block_sum<T>(c, x), acc[b]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) v[b] = tree<32>(acc[b]);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[b]), 16));
+    const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[b]), 48));
+    if (lane == 0 && b < live) {
+      const int32_t pk = toks[c0 + b];
+      a.h[(uint64_t) pk * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, a.w[pk]);
+    }
+  }
+}
+
+template <uint32_t T, int S, int L, int NB>
+__global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
+  using LD = GbLds<T, L, NB>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
+  constexpr int kThreads = kG1Threads;
+  constexpr uint32_t R = LD::D / 32 / (kThreads / 4);  // rounds that round a row of the largest dim
+  const uint32_t m = blockIdx.y, r0 = blockIdx.x * kG1Rows, n = a.n_tok * a.k;
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
+  const uint32_t per_seg = kG1Rows * rb / 16;
+  uint32_t idx[S];
+#pragma unroll
+  for (uint32_t u = 0; u < (uint32_t) S; u++) idx[u] = min(u * kThreads + threadIdx.x, per_seg - 1);
+  const uint32_t e = (uint32_t) a.ids[m];
+  // loads in the order they are waited on: the routing ids (the first 2 kThreads picks), the codebook, pick m's
+  // own x row (the owner pick is the expert's first: its token's row is the first pass's first), then the weights
+  const uint32_t* ids = (const uint32_t*) a.ids;
+  const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + kThreads;
+  const uint32_t id0 = ids[min(i0, n - 1)], id1 = ids[min(i1, n - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  GridStage<T, kThreads> gs;
+  grid_load(gs);
+  const float* xrow = a.x + (uint64_t) (m / a.k) * a.dim;
+  auto xval = [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return xrow + blk * 32 + c; };
+  Rounded8 rx[R];
+#pragma unroll
+  for (uint32_t r = 0; r < R; r++) round8_load<kThreads>(rx[r], xval, nblk, r * (kThreads / 4));
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t* sid = (uint32_t*) (smem + LD::ids);
+  if (i0 < n) sid[i0] = id0;
+  if (i1 < n) sid[i1] = id1;
+  // the expert's first pick owns the tile (the same decision in every thread)
+  int dup = (i0 < m && id0 == e) || (i1 < m && id1 == e);
+  for (uint32_t j = threadIdx.x + 2 * kThreads; j < m; j += kThreads) dup |= ids[j] == e;
+  if (__syncthreads_or(dup)) return;
+  const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
+  const u32x4* usrc = (const u32x4*) (a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb);
+  u32x4 wv[2 * S];
+#pragma unroll
+  for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = gsrc[idx[u]], wv[S + u] = usrc[idx[u]];
+  int32_t* toks = (int32_t*) (smem + LD::toks);  // [0, kMaxTok): the expert's picks in token order; [kMaxTok]: count
+  if (threadIdx.x < kWave) {  // wave 0, a lane a token: its pick of e if any, placed by the earlier tokens' count
+    int32_t pk = -1;
+    if (threadIdx.x < a.n_tok)
+      for (uint32_t j = 0; j < a.k; j++)
+        if ((n <= 2 * kThreads ? sid[threadIdx.x * a.k + j] : ids[threadIdx.x * a.k + j]) == e)
+          pk = (int32_t) (threadIdx.x * a.k + j);
+    const uint64_t has = __ballot(pk >= 0);
+    if (pk >= 0) toks[__builtin_popcountll(has & ((1ull << threadIdx.x) - 1))] = pk;
+    if (threadIdx.x == 0) toks[kMaxTok] = __builtin_popcountll(has);
+  }
+  int8_t* q = (int8_t*) (smem + LD::q);
+  float* d = (float*) (smem + LD::d);
+  grid_store(gs, smem + LD::grid);
+#pragma unroll
+  for (uint32_t r = 0; r < R; r++) round8_store<kThreads>(rx[r], nblk, r * (kThreads / 4), q, d);
+#pragma unroll
+  for (uint32_t u = 0; u < (uint32_t) S; u++) {
+    const uint32_t l = u * kThreads + threadIdx.x;
+    if (l < per_seg) {
+      ((u32x4*) (smem + LD::w))[l] = wv[u];
+      ((u32x4*) (smem + LD::w))[per_seg + l] = wv[S + u];
+    }
+  }
+  __syncthreads();
+  const int cnt = __builtin_amdgcn_readfirstlane(toks[kMaxTok]);
+  const auto* grid = (const typename GridOf<T>::E*) (smem + LD::grid);
+  const uint32_t lane = threadIdx.x % kWave, row = threadIdx.x / kWave;
+  const uint8_t* wr = smem + LD::w + ((lane / 32) * kG1Rows + row) * rb;
+  // the first pass holds the owner's row already; full passes while NB tokens are left, then a token a pass
+  int c0 = 0;
+  if (cnt >= NB) {
+    gub_pass<T, L, NB>(a, toks, 0, NB, 1, q, d, grid, wr, r0);
+    c0 = NB;
+  } else {
+    gub_pass<T, L, 1>(a, toks, 0, 1, 1, q, d, grid, wr, r0);
+    c0 = 1;
+  }
+  for (; c0 + NB <= cnt; c0 += NB) {
+    __syncthreads();  // (the previous pass's codes read)
+    gub_pass<T, L, NB>(a, toks, c0, NB, 0, q, d, grid, wr, r0);
+  }
+  for (; c0 < cnt; c0++) {
+    __syncthreads();
+    gub_pass<T, L, 1>(a, toks, c0, 1, 0, q, d, grid, wr, r0);
+  }
+}
+
 // S: staging slots a round (1, 2 or kPer: the fewest that hold the tile in one round)
 template <uint32_t T, int L, int S>
 __global__ __launch_bounds__(kDnThreads) void dn_kernel(DnArgs a) {

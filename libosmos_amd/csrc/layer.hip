@@ -43,6 +43,22 @@ bool gu1_launch_l(const GuArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess;
 }
 
+// the batch gate/up on gu1_kernel's tile (gub_kernel), NB tokens a pass
+template <uint32_t T, int L>
+bool gub_launch_l(const GuArgs& a, hipStream_t s) {
+  constexpr int NB = L == 16 ? 4 : 2;
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), words = fused::kG1Rows * rb / 16;
+  const dim3 grid(a.ff / fused::kG1Rows, a.n_tok * a.k);
+  constexpr int kT = fused::kG1Threads;
+  if (words <= (uint32_t) kT)
+    fused::gub_kernel<T, 1, L, NB><<<grid, kT, 0, s>>>(a);
+  else if (words <= 2u * kT)
+    fused::gub_kernel<T, 2, L, NB><<<grid, kT, 0, s>>>(a);
+  else
+    fused::gub_kernel<T, fused::kG1Slots, L, NB><<<grid, kT, 0, s>>>(a);
+  return hipGetLastError() == hipSuccess;
+}
+
 template <uint32_t T>
 bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
   *taken = false;
@@ -52,11 +68,11 @@ bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
     return true;
   if (a.dim % 512 == 0 && a.dim <= fused::G1Max<16>::dim) {
     *taken = true;
-    return gu1_launch_l<T, 16>(a, s);
+    return a.n_tok == 1 ? gu1_launch_l<T, 16>(a, s) : gub_launch_l<T, 16>(a, s);
   }
   if (a.dim % 1024 == 0 && a.dim >= 4096 && a.dim <= fused::G1Max<32>::dim) {
     *taken = true;
-    return gu1_launch_l<T, 32>(a, s);
+    return a.n_tok == 1 ? gu1_launch_l<T, 32>(a, s) : gub_launch_l<T, 32>(a, s);
   }
   return true;
 }
@@ -86,12 +102,10 @@ template <uint32_t T>
 bool gu_by(const GuArgs& a, hipStream_t s) {
   if (a.dim % Block<T>::values) return false;
   const bool wide = a.dim >= 4096;  // the contract's 32 lanes a row
-  if (a.n_tok == 1) {
-    bool taken = false;
-    const bool ok = gu1_launch<T>(a, s, &taken);
-    if (taken) return ok;
-    return wide ? gu_launch<T, 1, 32>(a, s) : gu_launch<T, 1, 16>(a, s);
-  }
+  bool taken = false;
+  const bool ok = gu1_launch<T>(a, s, &taken);
+  if (taken) return ok;
+  if (a.n_tok == 1) return wide ? gu_launch<T, 1, 32>(a, s) : gu_launch<T, 1, 16>(a, s);
   return wide ? gu_launch<T, 2, 32>(a, s) : gu_launch<T, 2, 16>(a, s);
 }
 

@@ -275,6 +275,51 @@ def test_lane_layer_one_token_types(g, name):
         assert (g.bits(g.host(out)) == g.bits(want)).all(), (name, dim)
 
 
+@pytest.mark.parametrize("name", ["IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ1_S", "IQ1_M", "Q2_K", "Q4_0", "Q4_K", "Q3_K"])
+def test_lane_layer_batch_types(g, name):
+    """a batch of 7 tokens over 6 experts (each expert picked by several tokens: the batch gate/up kernel's full and
+    one-token passes) for every lane type, dim 2048 (16 lanes a row) and 4096 (32), with a finite clamp: the oracle's
+    bits"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t = synth.ID[name]
+    for dim, ff in ((2048, 256), (4096, 512)):
+        n_exp, k, n_tok = 6, 3, 7
+        mk = synth.iq_blocks if name.startswith("IQ") else synth.random_blocks
+        gate = [mk(t, ff, dim, 700 + e) for e in range(n_exp)]
+        up = [mk(t, ff, dim, 800 + e) for e in range(n_exp)]
+        down = [mk(t, dim, ff, 900 + e) for e in range(n_exp)]
+        rng = np.random.default_rng(dim + 1)
+        x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+        ids, wts = _route(rng, n_tok, n_exp, k)
+        want = _lane_layer_oracle(t, x, ids, wts, gate, up, down, dim, ff, 1.5)
+        D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+        L = LaneLayer(t, t, dim, ff, n_exp, k, D(gate), D(up), D(down), lim=1.5)
+        out = torch.full((n_tok, dim), float("nan"), device="cuda")
+        print("batch layer", name, dim, flush=True)
+        L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+        assert (g.bits(g.host(out)) == g.bits(want)).all(), (name, dim)
+
+
+def test_lane_layer_largest_batch(g):
+    """the largest batch (64 tokens, top-10 of 16 experts: 640 picks, up to 64 tokens an expert): the oracle's bits"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t3 = synth.ID["IQ3_XXS"]
+    n_exp, k, dim, ff, n_tok = 16, 10, 1024, 256, 64
+    gate, up, down = _layer_case(t3, t3, n_exp, k, dim, ff, 21)
+    rng = np.random.default_rng(21)
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids, wts = _route(rng, n_tok, n_exp, k)
+    want = _lane_layer_oracle(t3, x, ids, wts, gate, up, down, dim, ff, math.inf)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(t3, t3, dim, ff, n_exp, k, D(gate), D(up), D(down))
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("largest batch layer", flush=True)
+    L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
+
+
 def _layer_case(tg, td, n_exp, k, dim, ff, seed):
     gate = [synth.iq_blocks(tg, ff, dim, seed + 1000 + e) for e in range(n_exp)]
     up = [synth.iq_blocks(tg, ff, dim, seed + 2000 + e) for e in range(n_exp)]
