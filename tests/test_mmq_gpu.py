@@ -43,7 +43,8 @@ def test_x8_rows(g, cols):
 
 @pytest.mark.parametrize("cols", [2048, 1280])
 def test_group(g, cols):
-    """three matrices at 1, 16 and 37 tokens (CT 4), then 64 tokens (two z tiles); one at a time; all the oracle's"""
+    """three matrices at 1, 16 and 37 tokens (two-tile passes and a last one-tile pass), then 64 tokens; then 5 and 33;
+    all the oracle's"""
     import torch
     rows = 64
     t = synth.ID["Q4_K"]
