@@ -8,9 +8,10 @@
 //
 // CDNA4 mapping: a workgroup owns 16 rows (their whole slab and the codebook staged in LDS once) x CT tiles of 16
 // tokens a pass. the integer half-dots are MFMAs: each 32-value block's codes (lane l: row l % 16, values 8 (l / 16) ..
-// + 7, decoded from LDS straight into its A operand - the IQ1 types' 8 grid + delta folded into one int8 per value)
-// go to two v_mfma_i32_16x16x32_i8, one with the second half's lanes zeroed, one with the first's: the two halves'
-// exact dots for 16 rows x 16 tokens. the float steps then run per output in the contract's order. the 4 waves split
+// + 7, decoded from LDS straight into its B operand - the IQ1 types' 8 grid + delta folded into one int8 per value;
+// the tokens' codes the A operand) go to two v_mfma_i32_16x16x32_i8, one with the second half's lanes zeroed, one
+// with the first's: the two halves' exact dots, D[token][row] - lane l holds tokens 4 (l / 16) + i of its own row
+// l % 16, so it applies that row's half scales itself. the float steps then run per output in the contract's order. the 4 waves split
 // the logical lanes (wave w the chains ll = w mod 4, blocks s = w mod 4), so a wave keeps L / 4 chains an output in
 // registers; the xor tree is finished across the waves through LDS with the same additions (fadd commutes exactly).
 #include "lanedec.h"
@@ -156,7 +157,9 @@ __device__ inline void scales<kIQ1_M>(lbytes b, int j, float& d, int& s0, int& s
   d = f16((a0 >> 12) | ((a1 >> 8) & 0x00F0) | ((a2 >> 4) & 0x0F00) | (a3 & 0xF000));
 }
 
-constexpr int kCT16 = 4, kCT32 = 2;  // token tiles a pass at 16 / 32 logical lanes (the waves' chains: 64 VGPRs)
+// token tiles a pass at 16 / 32 logical lanes (the waves' chains: 64 / 32 VGPRs; at 32 lanes a second tile's 32 more
+// cost more occupancy than its shared decode saves)
+constexpr int kCT16 = 4, kCT32 = 1;
 
 template <uint32_t T>
 constexpr uint32_t grid_bytes_of() {
@@ -167,13 +170,12 @@ constexpr uint32_t grid_bytes_of() {
 // and their partial trees
 template <uint32_t T, int CT>
 struct Lds {
-  uint32_t slab, grid, sm, scl, part, total;
+  uint32_t slab, grid, sm, part, total;
   __host__ __device__ Lds(uint32_t rb) {
     slab = 0;
     grid = (16 * rb + 15) / 16 * 16;
     sm = grid + grid_bytes_of<T>();
-    scl = sm + 128 * 8;
-    part = scl + kWaves * 2 * kTile * 4;
+    part = sm + 128 * 8;
     total = part + kWaves * CT * 4 * kWave * 4;
   }
 };
@@ -208,7 +210,6 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
   __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
   const uint64_t* sm = (const uint64_t*) (smem + L_.sm);
-  float* scl = (float*) (smem + L_.scl) + wave * 2 * kTile;  // [half][row]
   float* part = (float*) (smem + L_.part);                    // [wave][ct][i][lane]
   const uint8_t* arow = smem + L_.slab + col * rb;            // this lane's A row
   for (uint32_t c0 = 0; c0 < n; c0 += kTile * CT) {
@@ -259,32 +260,26 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
         chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
         const long a = (long) (((uint64_t) w1 << 32) | w0);
         const long a0 = quad < 2 ? a : 0, a1 = quad < 2 ? 0 : a;  // the first half's lanes, the second's
-        if (quad == 0) {  // lanes 0 .. 15: row col's ((d s21) / 8) per half (lane_part's first two products)
-          float dd;
-          int s0_, s1_;
-          scales<T>((lbytes) blk, j, dd, s0_, s1_);
-          scl[col] = __fmul_rn(__fmul_rn(dd, (float) s0_), 0.125f);
-          scl[kTile + col] = __fmul_rn(__fmul_rn(dd, (float) s1_), 0.125f);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float f0[4], f1[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) f0[i] = scl[4 * quad + i], f1[i] = scl[kTile + 4 * quad + i];
+        // row col's ((d s21) / 8) per half (lane_part's first two products): every lane its own row's
+        float dd;
+        int s0_, s1_;
+        scales<T>((lbytes) blk, j, dd, s0_, s1_);
+        const float f0 = __fmul_rn(__fmul_rn(dd, (float) s0_), 0.125f), f1 = __fmul_rn(__fmul_rn(dd, (float) s1_), 0.125f);
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) {
           if (ct < tiles) {
-            const v4i I0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bx[ct], v4i{0, 0, 0, 0}, 0, 0, 0);
-            const v4i I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bx[ct], v4i{0, 0, 0, 0}, 0, 0, 0);
+            // tokens the A operand, weight rows the B: D[token 4 quad + i][row col]
+            const v4i I0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(bx[ct], a0, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4i I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(bx[ct], a1, v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-              const float sub = __fadd_rn(__fmul_rn(f0[i], (float) I0[i]), __fmul_rn(f1[i], (float) I1[i]));
-              acc[c][ct][i] = __builtin_fmaf(xs[ct], sub, acc[c][ct][i]);
+              // token 4 quad + i's block scale, from the lane that loaded it (lane 4 quad + i: token col)
+              const float xt = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * quad + i) * 4, __float_as_int(xs[ct])));
+              const float sub = __fadd_rn(__fmul_rn(f0, (float) I0[i]), __fmul_rn(f1, (float) I1[i]));
+              acc[c][ct][i] = __builtin_fmaf(xt, sub, acc[c][ct][i]);
             }
           }
         }
-        __builtin_amdgcn_wave_barrier();  // the table read by every lane before the next block's is written
       }
     }
     // the tree's levels L/2 .. 4 within the wave: chains c and c ^ o4 (logical lanes ll and ll ^ 4 o4)
@@ -304,13 +299,13 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
     if (wave == 0) {  // levels 2 and 1: (T0 + T2) + (T1 + T3), T_w the wave's subtree (logical lanes w mod 4)
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) {
-        const uint32_t t = c0 + ct * kTile + col;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+          const uint32_t t = c0 + ct * kTile + 4 * quad + i;  // (D: token 4 quad + i, row col)
           const float* pp = part + (ct * 4 + i) * kWave + lane;
           const uint32_t wv = CT * 4 * kWave;  // a wave's stride
           const float v = __fadd_rn(__fadd_rn(pp[0], pp[2 * wv]), __fadd_rn(pp[wv], pp[3 * wv]));
-          if (t < n) y[(uint64_t) (r0 + t) * ys + row0 + 4 * quad + i] = v;
+          if (t < n) y[(uint64_t) (r0 + t) * ys + row0 + col] = v;
         }
       }
     }
