@@ -1,5 +1,6 @@
-"""Builds libosmos_amd/libosmos_mi355x.so: every csrc/*.hip compiled by hipcc for gfx950 (each file in its own
-process, in parallel), linked into one shared library whose exports are exactly include/**/*.h's declarations.
+"""Builds libosmos_amd/libosmos_mi355x.so: every csrc/*.hip compiled by hipcc for gfx950 and every csrc/*.cpp (host
+code: the GGUF reader) by the same compiler as plain C++ (each file in its own process, in parallel), linked into one
+shared library whose exports are exactly include/**/*.h's declarations.
 
 flags: -O3, -ffp-contract=off (every product and sum rounded on its own: the contracts' bits), packed-FP32 ops off
 (-Xclang -target-feature -Xclang -packed-fp32-ops), MFMA results in VGPRs (-mllvm -amdgpu-mfma-vgpr-form=1), -fPIC. run: python -m libosmos_amd.build
@@ -21,13 +22,18 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-fvisibility=h
          "-I" + os.path.join(os.path.dirname(HERE), "include")]
 
 
+HOST_FLAGS = ["-x", "c++", "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall",
+              "-I" + os.path.join(os.path.dirname(HERE), "include")]
+
+
 def sources():
-    return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def compile_one(src):
-    obj = os.path.join(OUT, src[:-4] + ".o")
-    cmd = [HIPCC] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    obj = os.path.join(OUT, src.rsplit(".", 1)[0] + ".o")
+    flags = FLAGS if src.endswith(".hip") else HOST_FLAGS
+    cmd = [HIPCC] + flags + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
     if r.returncode:

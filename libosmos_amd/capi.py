@@ -1,5 +1,5 @@
-"""ctypes bindings of libosmos_mi355x.so's C ABI (the declarations in include/osmos/gpu/*.h and
-include/osmos_mi355x.h), argument for argument: pointers are device addresses (a torch tensor's data_ptr() or a
+"""ctypes bindings of libosmos_mi355x.so's C ABI (the declarations in include/osmos/gpu/*.h, include/osmos/model/gguf.h
+and include/osmos_mi355x.h), argument for argument: pointers are device addresses (a torch tensor's data_ptr() or a
 hipMalloc'd address), `stream` a hipStream_t (torch.cuda.current_stream().cuda_stream) or None for the default.
 
 the library is never replaced by anything else: if libosmos_mi355x.so is missing, lib() raises - there is no CPU
@@ -74,6 +74,43 @@ SIGS.update({
     "osmos_lane_gate_up": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P]),
     "osmos_lane_down": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P]),
     "osmos_lane_group": (B, [U32, P, P, P, U32, U32, U32, U32, P, P, P, U32, P]),
+})
+
+
+
+# include/osmos/model/gguf.h (host memory: the GGUF reader touches no GPU)
+GGUF_ERR = 256
+GGUF_MAX_DIMS = 4
+
+
+class GgufValue(ctypes.Union):
+    _fields_ = [("u", ctypes.c_uint64), ("i", ctypes.c_int64), ("f", ctypes.c_double), ("s", ctypes.c_char_p),
+                ("items", P)]
+
+
+class GgufKv(ctypes.Structure):
+    _fields_ = [("key", ctypes.c_char_p), ("type", ctypes.c_int), ("item", ctypes.c_int), ("n", U64), ("v", GgufValue)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", U32), ("n_dims", U32), ("dims", U64 * GGUF_MAX_DIMS),
+                ("file", ctypes.c_int), ("offset", U64), ("bytes", U64)]
+
+
+class Gguf(ctypes.Structure):
+    _fields_ = [("n_files", ctypes.c_int), ("paths", ctypes.POINTER(ctypes.c_char_p)), ("sizes", ctypes.POINTER(U64)),
+                ("kv", ctypes.POINTER(GgufKv)), ("n_kv", ctypes.c_size_t), ("tensors", ctypes.POINTER(GgufTensor)),
+                ("n_tensors", ctypes.c_size_t)]
+
+
+SIGS.update({
+    "gguf_create": (ctypes.POINTER(Gguf), [ctypes.c_char_p, ctypes.c_char_p]),
+    "gguf_header": (ctypes.POINTER(Gguf), [ctypes.c_char_p, ctypes.c_char_p]),
+    "gguf_destroy": (None, [ctypes.POINTER(Gguf)]),
+    "gguf_tensor": (ctypes.POINTER(GgufTensor), [ctypes.POINTER(Gguf), ctypes.c_char_p]),
+    "gguf_kv": (ctypes.POINTER(GgufKv), [ctypes.POINTER(Gguf), ctypes.c_char_p]),
+    "gguf_bytes": (U64, [U32, U64]),
+    "gguf_int": (B, [ctypes.POINTER(GgufKv), ctypes.c_size_t, ctypes.POINTER(ctypes.c_int64)]),
 })
 
 _lib = None
