@@ -1,5 +1,5 @@
 /* libosmos MI355X: the element-wise ops the lane's expert path calls between its products (drop-in for those entries
-   of the reference's include/osmos/gpu/ops.h:111-117; the header's other ops are outside this library).
+   of the reference's include/osmos/gpu/ops.h:111-117, 123-124; the header's other ops are outside this library).
    contracts: reference include/osmos/gpu/ops.h:311-355. */
 #ifndef OSMOS_GPU_OPS_H
 #define OSMOS_GPU_OPS_H
@@ -21,6 +21,16 @@ bool ops_gather_rows(float *dst, const float *src, const int32_t *idx, uint32_t 
    order of src[idx[t m + j]], then add[t] added */
 bool ops_gather_sum_add(float *y, const float *src, const int32_t *idx, uint32_t m, uint32_t n, uint32_t dim,
                         const float *add, void *stream);
+
+/* replaces reference include/osmos/gpu/ops.h:123 (kernels/ops.hip:878-882): the stream held until *flag - host
+   memory the GPU maps (hipHostMalloc's) - holds value, or value with its top bit set (the host's mark of a failed
+   job); a system-scope acquire, so what the host wrote before the flag the kernels after see. the host must post
+   the value: the wait ends by itself only after about two hours (the reference's never). the lane's hand-off of
+   CPU-computed experts (reference src/run/hip_lane.c:218-219) */
+bool ops_wait(const uint32_t *flag, uint32_t value, void *stream);
+/* replaces reference include/osmos/gpu/ops.h:124 (kernels/ops.hip:884-889): rows idx[0 .. n) of src to the same rows
+   of dst, len floats a row (src may be host memory the GPU maps) */
+bool ops_copy_rows(float *dst, const float *src, const int32_t *idx, uint32_t n, uint32_t len, void *stream);
 
 #ifdef __cplusplus
 }

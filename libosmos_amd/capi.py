@@ -35,6 +35,8 @@ SIGS = {
     "q4x_expert_tiles": (B, [P, U32, U32, U32, U32, U32, P, P]),
     "q4x_moe_sum": (B, [P, P, P, U32, U32, U32, P, P, P, P]),
     "q4x_swiglu_rows": (B, [P, P, U32, P, U32, P, P, P]),
+    "ops_wait": (B, [P, U32, P]),
+    "ops_copy_rows": (B, [P, P, P, U32, U32, P]),
     "mm_known": (B, [U32]),
     "mm_fits": (B, [U32, U32, U32]),
     "mm_col_tiles": (U32, [U32, U32]),

@@ -205,6 +205,30 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(float* __restrict__ ds
   if (i < (uint64_t) n * len) dst[i] = src[(uint64_t) idx[i / len] * len + i % len];
 }
 
+// the stream held until *flag (host memory the GPU maps) holds value, or value with its top bit set (the host's mark of
+// a failed job) - one thread polling it with system-scope acquire loads (vector loads: never the scalar cache, which
+// would not see the host's store), a sleep between polls. the poll is bounded (2^32 polls of about 1.7 us: about two
+// hours) so the kernel always ends; the reference waits without bound (kernels/ops.hip:878-882)
+__global__ __launch_bounds__(64) void wait_kernel(const uint32_t* flag, uint32_t value) {
+  if (threadIdx.x) return;
+  const uint32_t marked = value | 0x80000000u;
+  for (uint32_t i = 0; i != 0xFFFFFFFFu; i++) {
+    const uint32_t v = __hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (v == value || v == marked) return;
+    __builtin_amdgcn_s_sleep(64);
+  }
+}
+
+// rows idx[0 .. n) of src copied to the same rows of dst, len floats a row (src may be mapped host memory)
+__global__ __launch_bounds__(256) void copy_rows_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                        const int32_t* __restrict__ idx, uint32_t n, uint32_t len) {
+  const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
+  if (i < (uint64_t) n * len) {
+    const uint64_t at = (uint64_t) idx[i / len] * len + i % len;
+    dst[at] = src[at];
+  }
+}
+
 // y[t][d] = sum over j in order of src[idx[t m + j]][d] (from 0), then add's (kernels/ops.hip:515-525); 4 values a thread
 __global__ __launch_bounds__(256) void gather_sum_kernel(float* __restrict__ y, const float* __restrict__ src,
                                                          const int32_t* __restrict__ idx, uint32_t m, uint32_t n,
@@ -375,6 +399,19 @@ extern "C" OSM_API bool ops_gather_rows(float* dst, const float* src, const int3
                                         void* stream) {
   if (!dst || !src || !idx || !n || !len) return false;
   moe::gather_rows_kernel<<<moe::grid256((uint64_t) n * len), 256, 0, (hipStream_t) stream>>>(dst, src, idx, n, len);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool ops_wait(const uint32_t* flag, uint32_t value, void* stream) {
+  if (!flag) return false;
+  moe::wait_kernel<<<1, 64, 0, (hipStream_t) stream>>>(flag, value);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool ops_copy_rows(float* dst, const float* src, const int32_t* idx, uint32_t n, uint32_t len,
+                                      void* stream) {
+  if (!dst || !src || !idx || !n || !len) return false;
+  moe::copy_rows_kernel<<<moe::grid256((uint64_t) n * len), 256, 0, (hipStream_t) stream>>>(dst, src, idx, n, len);
   return hipGetLastError() == hipSuccess;
 }
 

@@ -1,0 +1,62 @@
+"""ops_wait and ops_copy_rows (include/osmos/gpu/ops.h) on the MI355X: the lane's hand-off of rows a host job computes
+(reference src/run/hip_lane.c:218-219, include/osmos/gpu/ops.h:340-347). The stream is held while the host's flag
+holds anything but the value; released by the value with its top bit set (a failed job's mark); the rows the host
+wrote before the flag are what ops_copy_rows reads after it. The host always posts the value in the end (a timer, and
+a finally), so the wait ends in every outcome."""
+import threading
+import time
+
+import numpy as np
+import pytest
+
+from libosmos_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+
+def test_wait_then_copy_rows():
+    import torch
+    L = capi.lib()
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)  # (host memory the GPU maps)
+    rows, n = 64, 256
+    src = torch.zeros(rows, n, pin_memory=True)
+    dst = torch.full((rows, n), -1.0, device="cuda")
+    pick = [3, 7, 8, 63]
+    idx = torch.tensor(pick, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    release = threading.Timer(20.0, lambda: flag.fill_(7))
+    release.start()
+    print("ops_wait hand-off", flush=True)
+    try:
+        assert L.ops_wait(capi.addr(flag), 7, s.cuda_stream)
+        assert L.ops_copy_rows(capi.addr(dst), capi.addr(src), capi.addr(idx), len(pick), n, s.cuda_stream)
+        done = torch.cuda.Event()
+        done.record(s)
+        time.sleep(0.2)
+        assert not done.query(), "the stream ran past an unposted flag"
+        rng = np.random.default_rng(3)
+        want = rng.normal(0, 1, (rows, n)).astype(np.float32)
+        src.copy_(torch.from_numpy(want))  # the host job's rows, written before the flag
+        flag.fill_(5)  # another value: still held
+        time.sleep(0.1)
+        assert not done.query(), "the stream ran on a value that is not the one awaited"
+        flag.fill_(7 - (1 << 31))  # 7 with the top bit set: released
+        done.synchronize()
+    finally:
+        flag.fill_(7)
+        release.cancel()
+    torch.cuda.synchronize()
+    out = dst.cpu().numpy()
+    for r in range(rows):
+        if r in pick:
+            assert (out[r].view(np.int32) == want[r].view(np.int32)).all(), r
+        else:
+            assert (out[r] == -1.0).all(), r
+
+
+def test_refusals():
+    L = capi.lib()
+    assert not L.ops_wait(None, 1, None)
+    p = capi.ctypes.c_void_p(8)
+    assert not L.ops_copy_rows(None, p, p, 1, 1, None)
+    assert not L.ops_copy_rows(p, p, p, 0, 1, None) and not L.ops_copy_rows(p, p, p, 1, 0, None)
