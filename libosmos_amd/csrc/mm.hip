@@ -10,6 +10,8 @@
 // one 16-byte load from the tiled layout). A and B fill the same lane slots with the same columns, so the product is
 // the dot product whatever order the unit takes K in; the accumulator of a token depends on that token's column
 // alone, the K steps always in ascending order - the same bits at any batch size, tile count or grouping.
+#include <type_traits>
+
 #include "decode.h"
 #include "x16.h"
 
@@ -39,9 +41,49 @@ struct Args {
   float* y;
 };
 
-// blockIdx.x: 64 rows; blockIdx.y: the matrix; blockIdx.z: CT token tiles
-template <uint32_t T, int CT>
+// the codebook a type's decoder reads (Dec<T>::run's `tables`), held in LDS: only the members that type reads
+template <uint32_t T> struct LdsTab { struct { } g; };
+template <> struct LdsTab<kIQ2_XXS> { struct { uint64_t iq2xxs[256]; } g; };
+template <> struct LdsTab<kIQ2_XS> { struct { uint64_t iq2xs[512]; } g; };
+template <> struct LdsTab<kIQ2_S> { struct { uint64_t iq2s[1024]; } g; };
+template <> struct LdsTab<kIQ3_XXS> { struct { uint32_t iq3xxs[256]; } g; };
+template <> struct LdsTab<kIQ1_S> { struct { uint64_t iq1s[2048]; } g; };
+template <> struct LdsTab<kIQ1_M> { struct { uint64_t iq1s[2048]; } g; };
+template <> struct LdsTab<kIQ4_NL> { struct { } g; alignas(4) int8_t iq4nl[16]; };
+template <> struct LdsTab<kIQ4_XS> { struct { } g; alignas(4) int8_t iq4nl[16]; };
+
+template <uint32_t T>
+__device__ inline void fill_tab(LdsTab<T>& t) {  // every thread of the workgroup, from the constant tables
+  const uint32_t* src = nullptr;
+  uint32_t words = 0;
+  uint32_t* dst = (uint32_t*) &t;
+  if constexpr (T == kIQ2_XXS) src = (const uint32_t*) kDec.g.iq2xxs, words = sizeof t / 4;
+  else if constexpr (T == kIQ2_XS) src = (const uint32_t*) kDec.g.iq2xs, words = sizeof t / 4;
+  else if constexpr (T == kIQ2_S) src = (const uint32_t*) kDec.g.iq2s, words = sizeof t / 4;
+  else if constexpr (T == kIQ3_XXS) src = (const uint32_t*) kDec.g.iq3xxs, words = sizeof t / 4;
+  else if constexpr (T == kIQ1_S || T == kIQ1_M) src = (const uint32_t*) kDec.g.iq1s, words = sizeof t / 4;
+  else if constexpr (T == kIQ4_NL || T == kIQ4_XS) src = (const uint32_t*) kDec.iq4nl, words = 4, dst = (uint32_t*) t.iq4nl;
+  for (uint32_t i = threadIdx.x; i < words; i += kThreads) dst[i] = src[i];
+}
+
+// values a staged chunk of a row: whole blocks, about 256 bytes of a row (16 KB for the workgroup's 64 rows)
+template <uint32_t T>
+constexpr uint32_t chunk_values() {
+  constexpr uint32_t v = Block<T>::values, b = Block<T>::bytes, per256 = 256 / v * b;
+  return v == 1 ? 64 : per256 <= 72 ? 1024 : per256 <= 144 ? 512 : 256;
+}
+
+// blockIdx.x: 64 rows (a wave 16); blockIdx.y: the matrix; blockIdx.z: CT token tiles. the rows' bytes go through LDS a
+// chunk at a time (double-buffered: the next chunk's loads in flight while this one is decoded), W bytes a load (4
+// where every row's chunk is 4-aligned, else 2); the type's codebook is copied into LDS once. each wave decodes its 16
+// rows from LDS and runs the K steps in ascending order, as the unstaged kernel did: the same sums, the same bits
+template <uint32_t T, int CT, int W>
 __global__ __launch_bounds__(kThreads) void kernel(Args a) {
+  typedef typename std::conditional<W == 4, uint32_t, uint16_t>::type word;
+  constexpr uint32_t kCv = chunk_values<T>(), kCb = kCv / Block<T>::values * Block<T>::bytes;  // a row's chunk
+  constexpr uint32_t kWords = kRowsWg * kCb / W, kPer = (kWords + kThreads - 1) / kThreads;
+  __shared__ __attribute__((aligned(16))) uint8_t wbuf[2][kRowsWg * kCb];
+  __shared__ LdsTab<T> tab;
   const uint32_t m = blockIdx.y;
   const uint8_t* w = a.w0;
   const _Float16* x16 = a.x16;
@@ -52,29 +94,73 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     x16 += a.xoff[m], y += a.yoff[m];
   }
   const uint32_t t0 = blockIdx.z * kTile * CT, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const uint32_t row0 = blockIdx.x * kRowsWg + wave * kRowsWave;
-  if (t0 >= n || row0 >= a.rows) return;  // (uniform: the block's, then the wave's)
-  const uint32_t q = lane / 16;           // the lane's 8-value chunk of each 32-value step
-  const uint8_t* wr = w + (uint64_t) (row0 + lane % 16) * row_bytes<T>(a.cols);
+  const uint32_t rbase = blockIdx.x * kRowsWg, row0 = rbase + wave * kRowsWave;
+  if (t0 >= n) return;  // (uniform: the whole workgroup)
+  const bool live = row0 < a.rows;  // (a wave past the rows stages and meets the barriers, computes nothing)
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.cols), q = lane / 16;
+  // this thread's staged words: word i of the chunk is row i / (kCb / W), word i % (kCb / W) of it; its source a 32-bit
+  // byte offset from the matrix (one expert's matrix is far under 4 GB) plus the chunk's
+  constexpr uint32_t kWr = kCb / W;  // words a row's chunk
+  uint32_t woff[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; u++) {
+    const uint32_t i = min((uint32_t) (u * kThreads) + threadIdx.x, kWords - 1);
+    const uint32_t gr = min(rbase + i / kWr, a.rows - 1);  // (rows past the matrix: its last, staged and not used)
+    woff[u] = gr * rb + (i % kWr) * W;
+  }
+  word wr[kPer];
+  const uint32_t nch = (a.cols + kCv - 1) / kCv;
+  auto load = [&](uint32_t c) __attribute__((always_inline)) {
+    // (a short last chunk: the words past its end read its last word instead - loaded, never decoded)
+    const uint32_t lim = (a.cols - c * kCv) / Block<T>::values * Block<T>::bytes;  // the chunk's bytes a row
+    const uint8_t* base = w + (uint64_t) c * kCb;
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+      const uint32_t o = (u * kThreads + threadIdx.x) % kWr * W;
+      wr[u] = *(const word*) (base + woff[u] - (o < lim ? 0 : o - (lim - W)));
+    }
+  };
+  auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kPer; u++)
+      if (u * kThreads + threadIdx.x < kWords) ((word*) wbuf[buf])[u * kThreads + threadIdx.x] = wr[u];
+  };
+  fill_tab<T>(tab);
+  load(0);
+  store(0);
+  if (nch > 1) load(1);
+  __syncthreads();
   const _Float16* xb = x16 + x16_at(t0 + lane % 16, 8 * q, a.xts);
   f32x4 acc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ct++) acc[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (uint32_t k0 = 0; k0 < a.cols; k0 += kStep) {
-    float v[kChunk];
-    int k;
-    const uint8_t* b = chunk_at<T>(wr, k0 / kChunk + q, &k);
-    decode<T>(kDec, b, k, v);
-    half8 av;
+  for (uint32_t c = 0; c < nch; c++) {
+    const int buf = (int) (c % 2);
+    if (c + 1 < nch) store(buf ^ 1);  // (buffer buf ^ 1's last reads were before the previous barrier)
+    if (c + 2 < nch) load(c + 2);
+    const uint32_t k_end = min(kCv, a.cols - c * kCv);
+    const uint8_t* row = wbuf[buf] + (wave * kRowsWave + lane % 16) * kCb;
+    if (live) {
+      for (uint32_t k0 = 0; k0 < k_end; k0 += kStep) {
+        float v[kChunk];
+        int k;
+        const uint8_t* b = chunk_at<T>(row, k0 / kChunk + q, &k);
+        decode<T>(tab, b, k, v);
+        half8 av;
 #pragma unroll
-    for (int i = 0; i < kChunk; i++) av[i] = (_Float16) v[i];  // nearest, ties to even
+        for (int i = 0; i < kChunk; i++) av[i] = (_Float16) v[i];  // nearest, ties to even
+        const uint32_t kk = c * kCv + k0;
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++)
-      if (t0 + ct * kTile < n) {  // (uniform) the tiles that exist
-        const half8 bv = *(const half8*) (xb + (uint64_t) ct * kTile * a.xts + (k0 / 16) * 256);
-        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[ct], 0, 0, 0);
+        for (int ct = 0; ct < CT; ct++)
+          if (t0 + ct * kTile < n) {  // (uniform) the tiles that exist
+            const half8 bv = *(const half8*) (xb + (uint64_t) ct * kTile * a.xts + (kk / 16) * 256);
+            acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[ct], 0, 0, 0);
+          }
       }
+    }
+    __syncthreads();  // chunk c read by every wave; chunk c + 1 stored
   }
+  if (!live) return;
   // the accumulator: lane l holds rows 4 (l / 16) + i of the wave's 16, token l % 16 of the tile
 #pragma unroll
   for (int ct = 0; ct < CT; ct++) {
@@ -133,7 +219,14 @@ constexpr uint32_t col_tiles(uint32_t n) {
 template <uint32_t T, int CT>
 bool launch(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
   const dim3 grid((a.rows + kRowsWg - 1) / kRowsWg, n_mat, (max_n + kTile * CT - 1) / (kTile * CT));
-  kernel<T, CT><<<grid, kThreads, 0, s>>>(a);
+  // 4-byte staging loads where every row's chunk starts 4-aligned (the row bytes and the chunk bytes multiples of 4:
+  // the weights themselves come from hipMalloc, 256-aligned, or a caller's whole-block slice of them)
+  constexpr uint32_t cb = chunk_values<T>() / Block<T>::values * Block<T>::bytes;
+  const bool w4 = row_bytes<T>(a.cols) % 4 == 0 && cb % 4 == 0;
+  if (w4)
+    kernel<T, CT, 4><<<grid, kThreads, 0, s>>>(a);
+  else
+    kernel<T, CT, 2><<<grid, kThreads, 0, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
