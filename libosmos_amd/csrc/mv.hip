@@ -40,7 +40,7 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
   for (int q = 0; q < R; q++)
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[q][t] = 0.0f;
-#pragma unroll 2
+#pragma unroll(NT == 1 ? 8 : 2)  // (one token: the lane's chunks' loads all in flight at once)
   for (uint32_t c = lane; c < chunks; c += kHalf) {
     float v[R][kChunk];
 #pragma unroll
@@ -106,14 +106,15 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   rows_of<T, NT, R>(w[m], rows, cols, x + r0 * xs, xs, y + r0 * ys, ys, n < (uint32_t) NT ? n : NT);
 }
 
-constexpr int kR = 2;  // rows a half-wave: the tiling alone, never the bits
+// rows a half-wave: the tiling alone, never the bits (one token: a row a half-wave, for as many waves as the rows give)
+template <int NT> constexpr int rows_per() { return NT == 1 ? 1 : 2; }
 
 template <uint32_t T, int NT>
 bool run_nt(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t xs, uint32_t n_tok, float* y,
             uint32_t ys, hipStream_t s) {
-  constexpr uint32_t per = kWaves * 2 * kR;
+  constexpr uint32_t per = kWaves * 2 * rows_per<NT>();
   const dim3 grid((rows + per - 1) / per, (n_tok + NT - 1) / NT);
-  kernel<T, NT, kR><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+  kernel<T, NT, rows_per<NT>()><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -135,8 +136,8 @@ template <uint32_t T>
 bool group(const void* const* w, uint32_t n, uint32_t rows, uint32_t cols, const float* x, uint32_t x_mat,
            uint32_t x_div, float* y, hipStream_t s) {
   if (!w || !x || !y || cols % Block<T>::values || cols % kChunk || x_mat % kChunk || !x_div) return false;
-  constexpr uint32_t per = kWaves * 2 * kR;
-  group_kernel<T, kR><<<dim3((rows + per - 1) / per, n), kThreads, 0, s>>>((const uint8_t* const*) w, rows, cols, x,
+  constexpr uint32_t per = kWaves * 2 * rows_per<1>();
+  group_kernel<T, rows_per<1>()><<<dim3((rows + per - 1) / per, n), kThreads, 0, s>>>((const uint8_t* const*) w, rows, cols, x,
                                                                             x_mat, x_div, y);
   return hipGetLastError() == hipSuccess;
 }
@@ -144,8 +145,8 @@ bool group(const void* const* w, uint32_t n, uint32_t rows, uint32_t cols, const
 template <uint32_t T, int NT>
 bool group_tok_nt(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n, uint32_t rows,
                   uint32_t cols, const float* x, uint32_t xs, float* y, uint32_t ys, hipStream_t s) {
-  constexpr uint32_t per = kWaves * 2 * kR;
-  group_tok_kernel<T, NT, kR><<<dim3((rows + per - 1) / per, n), kThreads, 0, s>>>(
+  constexpr uint32_t per = kWaves * 2 * rows_per<NT>();
+  group_tok_kernel<T, NT, rows_per<NT>()><<<dim3((rows + per - 1) / per, n), kThreads, 0, s>>>(
       (const uint8_t* const*) w, cnt, xrow, rows, cols, x, xs, y, ys);
   return hipGetLastError() == hipSuccess;
 }
