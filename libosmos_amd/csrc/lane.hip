@@ -42,7 +42,7 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   float acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-#pragma unroll 2
+#pragma unroll(NT == 1 ? 4 : 2)  // (one token: 4 blocks' loads in flight)
   for (uint32_t s = ll; s < nblk; s += L) {
     Codes c;
     codes<T>(rb + (s / per) * Block<T>::bytes, (int) (s % per), c, const_grid<T>());
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(const uint8_t* const*
   float ag[NT], au[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.0f;
-#pragma unroll 2
+#pragma unroll(NT == 1 ? 4 : 2)  // (one token: 4 blocks' loads in flight)
   for (uint32_t s = ll; s < nblk; s += L) {
     Codes cg, cu;
     const uint64_t at = (s / per) * Block<T>::bytes;
