@@ -81,6 +81,8 @@ struct GuArgs {
   uint64_t gate_bytes, up_bytes;  // an expert's
   float lim;
   float* h;             // n_tok k rows of ff
+  const int8_t* xq;     // x already rounded (q8_round's codes and scales), for the kernels that take it: or null
+  const float* xd;
 };
 
 struct DnArgs {
@@ -91,6 +93,8 @@ struct DnArgs {
   uint64_t down_bytes;
   const float* add;
   float* out;           // n_tok rows of dim
+  const int8_t* hq;     // h already rounded (q8_round's codes and scales, rows by pick), for dn_kernel<.., P>
+  const float* hd;
 };
 
 // a workgroup's copy of segments into LDS, in two halves so that other loads can be issued between them: load()
@@ -433,7 +437,7 @@ __device__ __forceinline__ void gu_item(const GuArgs& a, uint32_t m, uint32_t ti
 }
 
 // one down tile: token t, rows tile * kDnRows .. + kDnRows
-template <uint32_t T, int S>
+template <uint32_t T, int S, bool P>
 __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t tile, uint8_t* smem, int L) {
   constexpr int kThreads = kDnThreads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
@@ -449,8 +453,21 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
   // the picks' expert ids first: the weights wait on them, and loads are waited for in issue order
   const int32_t pid = threadIdx.x < K ? a.ids[t * K + threadIdx.x] : 0;
   __builtin_amdgcn_sched_barrier(0);
+  // the token's k activation rows: rounded here, or (P) their codes and scales already rounded (the first two
+  // 16-byte words and the first scale a thread loaded now, the rest after the weights)
   Rounded8 rh;
-  round8_load<kThreads>(rh, hval, hblocks, 0);
+  u32x4 hw[2];
+  float hs = 0.0f;
+  const u32x4* hqs = (const u32x4*) (a.hq + (uint64_t) t * K * a.ff);
+  const float* hds = a.hd + (uint64_t) t * hblocks;
+  const uint32_t hwords = K * a.ff / 16;
+  if constexpr (P) {
+    hw[0] = hqs[min((uint32_t) threadIdx.x, hwords - 1)];
+    hw[1] = hqs[min((uint32_t) threadIdx.x + kThreads, hwords - 1)];
+    hs = hds[min((uint32_t) threadIdx.x, hblocks - 1)];
+  } else {
+    round8_load<kThreads>(rh, hval, hblocks, 0);
+  }
   const uint64_t o = (uint64_t) t * a.dim + r0 + threadIdx.x;
   const float addv = threadIdx.x < kDnRows ? a.add[o] : 0.0f;  // (loaded now: its latency off the tile's end)
   GridStage<T, kThreads, false> gs;  // (the full table: expanding it in 4 of the 16 waves is slower here)
@@ -479,15 +496,26 @@ __device__ __forceinline__ void dn_item(const DnArgs& a, uint32_t t, uint32_t ti
       if (j < K) picks[kMaxK + rank] = (int32_t) j;
     }
     grid_store(gs, smem + L_.grid);
-    round8_store<kThreads>(rh, hblocks, 0, q, d);
+    if constexpr (P) {
+      if (threadIdx.x < hwords) ((u32x4*) q)[threadIdx.x] = hw[0];
+      if (threadIdx.x + kThreads < hwords) ((u32x4*) q)[threadIdx.x + kThreads] = hw[1];
+      if (threadIdx.x < hblocks) d[threadIdx.x] = hs;
+    } else {
+      round8_store<kThreads>(rh, hblocks, 0, q, d);
+    }
     stage_store<kThreads, S>(st, smem + L_.w, nw, 0);
     for (uint32_t base = S * kThreads; base < nw; base += S * kThreads) {
       stage_load<kThreads, S>(st, wsrc, nw, per_seg, inv_seg, base);
       stage_store<kThreads, S>(st, smem + L_.w, nw, base);
     }
-    for (uint32_t base = kThreads / 4; base < hblocks; base += kThreads / 4) {
-      round8_load<kThreads>(rh, hval, hblocks, base);
-      round8_store<kThreads>(rh, hblocks, base, q, d);
+    if constexpr (P) {
+      for (uint32_t i = threadIdx.x + 2 * kThreads; i < hwords; i += kThreads) ((u32x4*) q)[i] = hqs[i];
+      for (uint32_t i = threadIdx.x + kThreads; i < hblocks; i += kThreads) d[i] = hds[i];
+    } else {
+      for (uint32_t base = kThreads / 4; base < hblocks; base += kThreads / 4) {
+        round8_load<kThreads>(rh, hval, hblocks, base);
+        round8_store<kThreads>(rh, hblocks, base, q, d);
+      }
     }
   }
   __syncthreads();
@@ -549,7 +577,7 @@ struct G1Lds {
 };
 
 // S: staging slots a matrix (the fewest that hold its tile rows); L: the contract's lanes a row (16 or 32)
-template <uint32_t T, int S, int L>
+template <uint32_t T, int S, int L, bool P = false>
 __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   using LD = G1Lds<T, L>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
@@ -567,11 +595,22 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   const float wm = a.w[m];
   GridStage<T, kThreads> gs;
   grid_load(gs);
-  Rounded8 rx[R];  // (the one token's row)
-  auto xval = [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return a.x + blk * 32 + c; };
+  // the one token's row: rounded here, or (P) its codes and scales already rounded, copied
+  constexpr int RQ = (int) (G1Max<L>::dim / 16 / kThreads) > 0 ? (int) (G1Max<L>::dim / 16 / kThreads) : 1;
+  Rounded8 rx[P ? 1 : R];
+  u32x4 xw[RQ];
+  float xs = 0.0f;
+  if constexpr (P) {
+    const uint32_t nw = a.dim / 16;
 #pragma unroll
-  for (int r = 0; r < R; r++)
-    if (r == 0 || (uint32_t) r * (kThreads / 4) < nblk) round8_load<kThreads>(rx[r], xval, nblk, r * (kThreads / 4));
+    for (int r = 0; r < RQ; r++) xw[r] = ((const u32x4*) a.xq)[min(r * kThreads + threadIdx.x, nw - 1)];
+    xs = a.xd[min((uint32_t) threadIdx.x, nblk - 1)];  // (nblk <= 256 = kThreads)
+  } else {
+    auto xval = [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return a.x + blk * 32 + c; };
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      if (r == 0 || (uint32_t) r * (kThreads / 4) < nblk) round8_load<kThreads>(rx[r], xval, nblk, r * (kThreads / 4));
+  }
   // (a scheduling barrier: the codebook and x loads issue before the id is waited for)
   __builtin_amdgcn_sched_barrier(0);
   const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
@@ -582,9 +621,16 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   int8_t* q = (int8_t*) (smem + LD::q);
   float* d = (float*) (smem + LD::d);
   grid_store(gs, smem + LD::grid);
+  if constexpr (P) {
 #pragma unroll
-  for (int r = 0; r < R; r++)
-    if (r == 0 || (uint32_t) r * (kThreads / 4) < nblk) round8_store<kThreads>(rx[r], nblk, r * (kThreads / 4), q, d);
+    for (int r = 0; r < RQ; r++)
+      if (r * kThreads + threadIdx.x < a.dim / 16) ((u32x4*) q)[r * kThreads + threadIdx.x] = xw[r];
+    if (threadIdx.x < nblk) d[threadIdx.x] = xs;
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; r++)
+      if (r == 0 || (uint32_t) r * (kThreads / 4) < nblk) round8_store<kThreads>(rx[r], nblk, r * (kThreads / 4), q, d);
+  }
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) {
     const uint32_t l = u * kThreads + threadIdx.x;
@@ -829,10 +875,10 @@ __global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
 }
 
 // S: staging slots a round (1, 2 or kPer: the fewest that hold the tile in one round)
-template <uint32_t T, int L, int S>
+template <uint32_t T, int L, int S, bool P = false>
 __global__ __launch_bounds__(kDnThreads) void dn_kernel(DnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  dn_item<T, S>(a, blockIdx.y, blockIdx.x, smem, L);
+  dn_item<T, S, P>(a, blockIdx.y, blockIdx.x, smem, L);
 }
 
 }  // namespace fused

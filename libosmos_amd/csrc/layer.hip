@@ -6,6 +6,7 @@
 
 extern "C" {
 #include "../../include/osmos_mi355x.h"
+#include "../../include/osmos/gpu/q8.h"
 }
 
 namespace osm {
@@ -34,6 +35,17 @@ bool gu1_launch_l(const GuArgs& a, hipStream_t s) {
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), words = fused::kG1Rows * rb / 16;
   const dim3 grid(a.ff / fused::kG1Rows, a.k);
   constexpr int kT = fused::kG1Threads;
+  if constexpr (L == 32) {  // (x already rounded: the P kernels copy it)
+    if (a.xq) {
+      if (words <= (uint32_t) kT)
+        fused::gu1_kernel<T, 1, L, true><<<grid, kT, 0, s>>>(a);
+      else if (words <= 2u * kT)
+        fused::gu1_kernel<T, 2, L, true><<<grid, kT, 0, s>>>(a);
+      else
+        fused::gu1_kernel<T, fused::kG1Slots, L, true><<<grid, kT, 0, s>>>(a);
+      return hipGetLastError() == hipSuccess;
+    }
+  }
   if (words <= (uint32_t) kT)
     fused::gu1_kernel<T, 1, L><<<grid, kT, 0, s>>>(a);
   else if (words <= 2u * kT)
@@ -79,7 +91,7 @@ bool gu1_launch(const GuArgs& a, hipStream_t s, bool* taken) {
 
 template <uint32_t T, int L, int S>
 bool dn_launch_s(const DnArgs& a, hipStream_t s, uint32_t lds) {
-  auto k = fused::dn_kernel<T, L, S>;
+  auto k = a.hq ? fused::dn_kernel<T, L, S, true> : fused::dn_kernel<T, L, S>;  // (h already rounded: copied)
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds) != hipSuccess)
     return false;
@@ -137,8 +149,20 @@ bool dn(uint32_t type, const DnArgs& a, hipStream_t s) {
   }
 }
 
-// the workspace: h, a row of ff floats a pick
-uint64_t h_bytes(const OsmosLaneLayer* L, uint32_t n_tok) { return ((uint64_t) n_tok * L->k * L->ff * 4 + 255) / 256 * 256; }
+// the workspace: h, a row of ff floats a pick; where rounding x or h once beats each workgroup rounding all of it
+// (one token at dim >= 4096: every gate/up tile rounds the token's whole row; k ff > 8192: every down tile rounds all
+// of its token's activations), their rounded codes and scales (q8_round's) after it, each part 256-aligned
+uint64_t a256(uint64_t b) { return (b + 255) / 256 * 256; }
+uint64_t h_bytes(const OsmosLaneLayer* L, uint32_t n_tok) { return a256((uint64_t) n_tok * L->k * L->ff * 4); }
+bool round_x(const OsmosLaneLayer* L, uint32_t n_tok) { return n_tok == 1 && L->dim >= 4096; }
+bool round_h(const OsmosLaneLayer* L) { return L->k * L->ff > 8192; }
+uint64_t x_part(const OsmosLaneLayer* L, uint32_t n_tok) {
+  return round_x(L, n_tok) ? a256((uint64_t) n_tok * L->dim) + a256((uint64_t) n_tok * L->dim / 32 * 4) : 0;
+}
+uint64_t h_part(const OsmosLaneLayer* L, uint32_t n_tok) {
+  const uint64_t n = (uint64_t) n_tok * L->k * L->ff;
+  return round_h(L) ? a256(n) + a256(n / 32 * 4) : 0;
+}
 
 }  // namespace layer
 }  // namespace osm
@@ -147,7 +171,7 @@ using namespace osm;
 
 extern "C" OSM_API uint64_t osmos_lane_workspace(const OsmosLaneLayer* L, uint32_t n_tok) {
   if (!L || !n_tok || !L->k) return 0;
-  return layer::h_bytes(L, n_tok);
+  return layer::h_bytes(L, n_tok) + layer::x_part(L, n_tok) + layer::h_part(L, n_tok);
 }
 
 namespace {
@@ -164,14 +188,15 @@ extern "C" OSM_API bool osmos_lane_gate_up(const OsmosLaneLayer* L, const float*
                                            const float* w, float* h, void* stream) {
   if (!layer_ok(L, n_tok) || !x || !ids || !w || !h || (uintptr_t) h % 16) return false;
   const fused::GuArgs ga = {x, ids, w, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->gate, (const uint8_t*) L->up,
-                            L->gate_bytes, L->up_bytes, L->lim, h};
+                            L->gate_bytes, L->up_bytes, L->lim, h, nullptr, nullptr};
   return layer::gu(L->type_gu, ga, (hipStream_t) stream);
 }
 
 extern "C" OSM_API bool osmos_lane_down(const OsmosLaneLayer* L, const float* h, uint32_t n_tok, const int32_t* ids,
                                         const float* add, float* out, void* stream) {
   if (!layer_ok(L, n_tok) || !h || !ids || !add || !out || (uintptr_t) h % 16) return false;
-  const fused::DnArgs da = {h, ids, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->down, L->down_bytes, add, out};
+  const fused::DnArgs da = {h, ids, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->down, L->down_bytes, add, out,
+                            nullptr, nullptr};
   return layer::dn(L->type_down, da, (hipStream_t) stream);
 }
 
@@ -180,5 +205,27 @@ extern "C" OSM_API bool osmos_lane_layer(const OsmosLaneLayer* L, const float* x
                                          uint64_t workspace_bytes, void* stream) {
   if (!layer_ok(L, n_tok) || !workspace || workspace_bytes < osmos_lane_workspace(L, n_tok)) return false;
   float* h = (float*) workspace;
-  return osmos_lane_gate_up(L, x, n_tok, ids, w, h, stream) && osmos_lane_down(L, h, n_tok, ids, add, out, stream);
+  uint8_t* at = (uint8_t*) workspace + layer::h_bytes(L, n_tok);
+  const hipStream_t s = (hipStream_t) stream;
+  int8_t* xq = nullptr;
+  float* xd = nullptr;
+  if (layer::round_x(L, n_tok)) {  // x rounded once (the same bits as the kernels' own rounding: q8_round's)
+    xq = (int8_t*) at, at += layer::a256((uint64_t) n_tok * L->dim);
+    xd = (float*) at, at += layer::a256((uint64_t) n_tok * L->dim / 32 * 4);
+    if (!q8_round(x, n_tok, L->dim, L->dim, xq, xd, stream)) return false;
+  }
+  const fused::GuArgs ga = {x, ids, w, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->gate, (const uint8_t*) L->up,
+                            L->gate_bytes, L->up_bytes, L->lim, h, xq, xd};
+  if (!layer::gu(L->type_gu, ga, s)) return false;
+  int8_t* hq = nullptr;
+  float* hd = nullptr;
+  if (layer::round_h(L)) {  // h rounded once, rows by pick (down's rounding: q8_round's)
+    const uint64_t n = (uint64_t) n_tok * L->k * L->ff;
+    hq = (int8_t*) at, at += layer::a256(n);
+    hd = (float*) at;
+    if (!q8_round(h, n_tok * L->k, L->ff, L->ff, hq, hd, stream)) return false;
+  }
+  const fused::DnArgs da = {h, ids, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->down, L->down_bytes, add, out,
+                            hq, hd};
+  return layer::dn(L->type_down, da, s);
 }
