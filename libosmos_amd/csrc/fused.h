@@ -706,7 +706,7 @@ struct GbLds {
 
 // one pass of gub_kernel: tokens toks[c0 .. c0 + live) (live <= NB), x rows from..NB-1 rounded into q/d (the rows
 // before from are there already), chains, trees and h
-template <uint32_t T, int L, int NB>
+template <uint32_t T, int L, int NB, bool P>
 __device__ __forceinline__ void gub_pass(const GuArgs& a, const int32_t* toks, int c0, int live, int from, int8_t* q,
                                          float* d, const typename GridOf<T>::E* grid, const uint8_t* wr, uint32_t r0) {
   constexpr int kThreads = kG1Threads;
@@ -718,10 +718,22 @@ __device__ __forceinline__ void gub_pass(const GuArgs& a, const int32_t* toks, i
     const uint32_t b = blk / nblk, tb = (int) b < live ? b : (uint32_t) live - 1;
     return a.x + (uint64_t) ((uint32_t) toks[c0 + (int) tb] / a.k) * a.dim + (blk % nblk) * 32 + c;
   };
-  for (uint32_t base = from * nblk; base < NB * nblk; base += kThreads / 4) {
-    Rounded8 rx;
-    round8_load<kThreads>(rx, xval, NB * nblk, base);
-    round8_store<kThreads>(rx, NB * nblk, base, q, d);
+  if constexpr (P) {  // (x already rounded: the rows' codes and scales copied)
+    const uint32_t wpr = a.dim / 16;
+    for (uint32_t i = from * wpr + threadIdx.x; i < NB * wpr; i += kThreads) {
+      const uint32_t b = i / wpr, tb = (int) b < live ? b : (uint32_t) live - 1;
+      ((u32x4*) q)[i] = ((const u32x4*) (a.xq + (uint64_t) ((uint32_t) toks[c0 + (int) tb] / a.k) * a.dim))[i % wpr];
+    }
+    for (uint32_t i = from * nblk + threadIdx.x; i < NB * nblk; i += kThreads) {
+      const uint32_t b = i / nblk, tb = (int) b < live ? b : (uint32_t) live - 1;
+      d[i] = a.xd[(uint64_t) ((uint32_t) toks[c0 + (int) tb] / a.k) * nblk + i % nblk];
+    }
+  } else {
+    for (uint32_t base = from * nblk; base < NB * nblk; base += kThreads / 4) {
+      Rounded8 rx;
+      round8_load<kThreads>(rx, xval, NB * nblk, base);
+      round8_store<kThreads>(rx, NB * nblk, base, q, d);
+    }
   }
   __syncthreads();
   float v[NB];
@@ -787,7 +799,7 @@ __device__ __forceinline__ void gub_pass(const GuArgs& a, const int32_t* toks, i
   }
 }
 
-template <uint32_t T, int S, int L, int NB>
+template <uint32_t T, int S, int L, int NB, bool P = false>
 __global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
   using LD = GbLds<T, L, NB>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
@@ -810,9 +822,19 @@ __global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
   grid_load(gs);
   const float* xrow = a.x + (uint64_t) (m / a.k) * a.dim;
   auto xval = [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return xrow + blk * 32 + c; };
-  Rounded8 rx[R];
+  Rounded8 rx[P ? 1 : R];
+  constexpr int RQ = (int) (LD::D / 16 / kThreads) > 0 ? (int) (LD::D / 16 / kThreads) : 1;
+  u32x4 xw[RQ];
+  float xs = 0.0f;
+  if constexpr (P) {  // (x already rounded: the owner's row's codes and scales, copied)
+    const u32x4* src = (const u32x4*) (a.xq + (uint64_t) (m / a.k) * a.dim);
 #pragma unroll
-  for (uint32_t r = 0; r < R; r++) round8_load<kThreads>(rx[r], xval, nblk, r * (kThreads / 4));
+    for (int r = 0; r < RQ; r++) xw[r] = src[min(r * kThreads + threadIdx.x, a.dim / 16 - 1)];
+    xs = a.xd[(uint64_t) (m / a.k) * nblk + min((uint32_t) threadIdx.x, nblk - 1)];
+  } else {
+#pragma unroll
+    for (uint32_t r = 0; r < R; r++) round8_load<kThreads>(rx[r], xval, nblk, r * (kThreads / 4));
+  }
   __builtin_amdgcn_sched_barrier(0);
   uint32_t* sid = (uint32_t*) (smem + LD::ids);
   if (i0 < n) sid[i0] = id0;
@@ -840,8 +862,15 @@ __global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
   int8_t* q = (int8_t*) (smem + LD::q);
   float* d = (float*) (smem + LD::d);
   grid_store(gs, smem + LD::grid);
+  if constexpr (P) {
 #pragma unroll
-  for (uint32_t r = 0; r < R; r++) round8_store<kThreads>(rx[r], nblk, r * (kThreads / 4), q, d);
+    for (int r = 0; r < RQ; r++)
+      if (r * kThreads + threadIdx.x < a.dim / 16) ((u32x4*) q)[r * kThreads + threadIdx.x] = xw[r];
+    if (threadIdx.x < nblk) d[threadIdx.x] = xs;
+  } else {
+#pragma unroll
+    for (uint32_t r = 0; r < R; r++) round8_store<kThreads>(rx[r], nblk, r * (kThreads / 4), q, d);
+  }
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) {
     const uint32_t l = u * kThreads + threadIdx.x;
@@ -858,19 +887,19 @@ __global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
   // the first pass holds the owner's row already; full passes while NB tokens are left, then a token a pass
   int c0 = 0;
   if (cnt >= NB) {
-    gub_pass<T, L, NB>(a, toks, 0, NB, 1, q, d, grid, wr, r0);
+    gub_pass<T, L, NB, P>(a, toks, 0, NB, 1, q, d, grid, wr, r0);
     c0 = NB;
   } else {
-    gub_pass<T, L, 1>(a, toks, 0, 1, 1, q, d, grid, wr, r0);
+    gub_pass<T, L, 1, P>(a, toks, 0, 1, 1, q, d, grid, wr, r0);
     c0 = 1;
   }
   for (; c0 + NB <= cnt; c0 += NB) {
     __syncthreads();  // (the previous pass's codes read)
-    gub_pass<T, L, NB>(a, toks, c0, NB, 0, q, d, grid, wr, r0);
+    gub_pass<T, L, NB, P>(a, toks, c0, NB, 0, q, d, grid, wr, r0);
   }
   for (; c0 < cnt; c0++) {
     __syncthreads();
-    gub_pass<T, L, 1>(a, toks, c0, 1, 0, q, d, grid, wr, r0);
+    gub_pass<T, L, 1, P>(a, toks, c0, 1, 0, q, d, grid, wr, r0);
   }
 }
 
