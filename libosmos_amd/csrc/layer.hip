@@ -62,7 +62,7 @@ bool gub_launch_l(const GuArgs& a, hipStream_t s) {
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), words = fused::kG1Rows * rb / 16;
   const dim3 grid(a.ff / fused::kG1Rows, a.n_tok * a.k);
   constexpr int kT = fused::kG1Threads;
-  if constexpr (L == 32) {  // (x already rounded: the P kernels copy it)
+  {  // (x already rounded: the P kernels copy it)
     if (a.xq) {
       if (words <= (uint32_t) kT)
         fused::gub_kernel<T, 1, L, NB, true><<<grid, kT, 0, s>>>(a);
@@ -161,18 +161,18 @@ bool dn(uint32_t type, const DnArgs& a, hipStream_t s) {
 }
 
 // the workspace: h, a row of ff floats a pick; where rounding x or h once beats each workgroup rounding all of it
-// (dim >= 4096: every gate/up tile rounds its tokens' whole rows; k ff > 8192: every down tile rounds all
+// (dim >= 4096 or 16 tokens and more: every gate/up tile rounds its tokens' whole rows; k ff > 8192: every down tile rounds all
 // of its token's activations), their rounded codes and scales (q8_round's) after it, each part 256-aligned
 uint64_t a256(uint64_t b) { return (b + 255) / 256 * 256; }
 uint64_t h_bytes(const OsmosLaneLayer* L, uint32_t n_tok) { return a256((uint64_t) n_tok * L->k * L->ff * 4); }
-bool round_x(const OsmosLaneLayer* L, uint32_t) { return L->dim >= 4096; }
-bool round_h(const OsmosLaneLayer* L) { return L->k * L->ff > 8192; }
+bool round_x(const OsmosLaneLayer* L, uint32_t n_tok) { return L->dim >= 4096 || n_tok >= 16; }
+bool round_h(const OsmosLaneLayer* L, uint32_t n_tok) { return L->k * L->ff > 8192 || n_tok >= 16; }
 uint64_t x_part(const OsmosLaneLayer* L, uint32_t n_tok) {
   return round_x(L, n_tok) ? a256((uint64_t) n_tok * L->dim) + a256((uint64_t) n_tok * L->dim / 32 * 4) : 0;
 }
 uint64_t h_part(const OsmosLaneLayer* L, uint32_t n_tok) {
   const uint64_t n = (uint64_t) n_tok * L->k * L->ff;
-  return round_h(L) ? a256(n) + a256(n / 32 * 4) : 0;
+  return round_h(L, n_tok) ? a256(n) + a256(n / 32 * 4) : 0;
 }
 
 }  // namespace layer
@@ -230,7 +230,7 @@ extern "C" OSM_API bool osmos_lane_layer(const OsmosLaneLayer* L, const float* x
   if (!layer::gu(L->type_gu, ga, s)) return false;
   int8_t* hq = nullptr;
   float* hd = nullptr;
-  if (layer::round_h(L)) {  // h rounded once, rows by pick (down's rounding: q8_round's)
+  if (layer::round_h(L, n_tok)) {  // h rounded once, rows by pick (down's rounding: q8_round's)
     const uint64_t n = (uint64_t) n_tok * L->k * L->ff;
     hq = (int8_t*) at, at += layer::a256(n);
     hd = (float*) at;
