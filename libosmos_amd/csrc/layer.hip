@@ -6,7 +6,6 @@
 
 extern "C" {
 #include "../../include/osmos_mi355x.h"
-#include "../../include/osmos/gpu/q8.h"
 }
 
 namespace osm {
