@@ -185,8 +185,21 @@ extern "C" OSM_API uint64_t osmos_lane_workspace(const OsmosLaneLayer* L, uint32
 }
 
 namespace {
+uint32_t block_values(uint32_t type) {  // a lane type's values a block (0: not a lane type)
+  switch (type) {
+#define X(t) \
+  case t: return Block<t>::values;
+    OSM_LANE_TYPES(X)
+#undef X
+    default: return 0;
+  }
+}
+
+// every check before anything is queued: a refused layer queues nothing (a shape only the down half refuses included)
 bool layer_ok(const OsmosLaneLayer* L, uint32_t n_tok) {
-  return L && n_tok && L->k && L->dim && L->ff && L->n_exp && L->gate && L->up && L->down && n_tok <= fused::kMaxTok &&
+  const uint32_t vg = L ? block_values(L->type_gu) : 0, vd = L ? block_values(L->type_down) : 0;
+  return L && vg && vd && L->dim % vg == 0 && L->ff % vd == 0 && n_tok && L->k && L->dim && L->ff && L->n_exp &&
+         L->gate && L->up && L->down && n_tok <= fused::kMaxTok &&
          L->k <= fused::kMaxK && L->dim % 32 == 0 && L->ff % fused::kGuRowsMax == 0 && L->ff % 32 == 0 &&
          L->dim % fused::kDnRows == 0 &&
          ((uintptr_t) L->gate | (uintptr_t) L->up | (uintptr_t) L->down | L->gate_bytes | L->up_bytes | L->down_bytes) %

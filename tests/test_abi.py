@@ -53,3 +53,20 @@ def test_refusals_without_gpu(built):
     assert not L.mv_run(99, None, 16, 512, None, 1, None, None)
     assert not L.quant_known(99)
     assert L.quant_known(18)
+
+
+def test_layer_refuses_before_queueing(built):
+    """osmos_lane_layer / _gate_up / _down check every shape first - a down matrix of rows that are not whole blocks
+    (ff 384 in IQ3_XXS's 256-value blocks), a gate/up type that is not a lane type - so a refused call queues nothing
+    (no launch happens: these run without a GPU)"""
+    L = built
+    p = 1 << 20  # (16-aligned stand-in addresses: never read, the calls refuse first)
+    P = capi.ctypes.c_void_p
+
+    def layer(tg, td, dim, ff):
+        return capi.OsmosLaneLayer(tg, td, dim, ff, 8, 2, float("inf"), p, p, p, 1 << 16, 1 << 16, 1 << 16)
+    for d in (layer(18, 18, 3072, 384), layer(18, 16, 2048, 384), layer(1, 18, 2048, 512), layer(18, 99, 2048, 512)):
+        ws = L.osmos_lane_workspace(capi.ctypes.byref(d), 1)
+        assert not L.osmos_lane_layer(capi.ctypes.byref(d), P(p), 1, P(p), P(p), P(p), P(p), P(p), max(ws, 1 << 20), None)
+        assert not L.osmos_lane_gate_up(capi.ctypes.byref(d), P(p), 1, P(p), P(p), P(p), None)
+        assert not L.osmos_lane_down(capi.ctypes.byref(d), P(p), 1, P(p), P(p), P(p), None)

@@ -301,6 +301,27 @@ def test_lane_layer_batch_types(g, name):
         assert (g.bits(g.host(out)) == g.bits(want)).all(), (name, dim)
 
 
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_lane_layer_other_dims(g, n_tok):
+    """a hidden size outside the one-token / batch tiles' ranges (3072: between 2048 and 4096) - the general gate/up
+    kernel: the oracle's bits"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    t3 = synth.ID["IQ3_XXS"]
+    n_exp, k, dim, ff = 8, 3, 3072, 512
+    gate, up, down = _layer_case(t3, t3, n_exp, k, dim, ff, 31)
+    rng = np.random.default_rng(31 + n_tok)
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids, wts = _route(rng, n_tok, n_exp, k)
+    want = _lane_layer_oracle(t3, x, ids, wts, gate, up, down, dim, ff, 1.25)
+    D = lambda ms: g.dev(np.stack(ms)).reshape(n_exp, -1)  # noqa: E731
+    L = LaneLayer(t3, t3, dim, ff, n_exp, k, D(gate), D(up), D(down), lim=1.25)
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("other dims layer", n_tok, flush=True)
+    L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
+
+
 def test_lane_layer_largest_batch(g):
     """the largest batch (64 tokens, top-10 of 16 experts: 640 picks, up to 64 tokens an expert): the oracle's bits"""
     import torch
