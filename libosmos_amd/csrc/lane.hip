@@ -126,6 +126,33 @@ __global__ __launch_bounds__(kThreads) void round_kernel(const float* __restrict
   if (i == 0) d[(uint64_t) r * nblk + s] = __fdiv_rn(a, 127.0f);
 }
 
+// the same rounding with 4 lanes a block, 8 values a lane (two 16-byte loads, one 8-byte store): for x rows 16-aligned
+// and q 8-aligned. each value's code is rintf(v * inv) as above; the block's max by a 2-step exchange of the 4 lanes'
+__global__ __launch_bounds__(kThreads) void round8_kernel(const float* __restrict__ x, uint32_t rows, uint32_t cols,
+                                                          uint32_t xs, int8_t* __restrict__ q, float* __restrict__ d) {
+  const uint32_t nblk = cols / 32;
+  const uint64_t blk = ((uint64_t) blockIdx.x * kThreads + threadIdx.x) / 4;
+  const uint32_t c = threadIdx.x % 4;
+  const uint64_t nb = (uint64_t) rows * nblk, b = blk < nb ? blk : nb - 1;  // (past the end: the last block, no stores)
+  const uint32_t r = (uint32_t) (b / nblk), s = (uint32_t) (b % nblk);
+  const float4* src = (const float4*) (x + (uint64_t) r * xs + (uint64_t) s * 32 + 8 * c);
+  const float4 lo = src[0], hi = src[1];
+  const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+  a = fmaxf(a, __shfl_xor(a, 1, 4));
+  a = fmaxf(a, __shfl_xor(a, 2, 4));
+  const float inv = a > 0.0f ? __fdiv_rn(127.0f, a) : 0.0f;
+  uint64_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) w |= (uint64_t) (uint8_t) (int8_t) (int) rintf(__fmul_rn(v[i], inv)) << (8 * i);
+  if (blk < nb) {
+    *(uint64_t*) (q + (uint64_t) r * cols + (uint64_t) s * 32 + 8 * c) = w;
+    if (c == 0) d[(uint64_t) r * nblk + s] = __fdiv_rn(a, 127.0f);
+  }
+}
+
 // ---- dispatch ----
 struct Args {
   const void* const *wg, *const *wu;
@@ -197,7 +224,14 @@ using namespace osm;
 extern "C" OSM_API bool q8_round(const float* x, uint32_t rows, uint32_t cols, uint32_t xs, int8_t* q, float* d,
                          void* stream) {
   if (!x || !q || !d || !rows || !cols || cols % 32 || xs < cols) return false;
-  const uint64_t blocks = (uint64_t) rows * (cols / 32), per = lane::kThreads / 32;
+  const uint64_t blocks = (uint64_t) rows * (cols / 32);
+  if ((uintptr_t) x % 16 == 0 && xs % 4 == 0 && (uintptr_t) q % 8 == 0) {  // (the vector form where it is aligned)
+    const uint64_t per8 = lane::kThreads / 4;
+    lane::round8_kernel<<<(unsigned) ((blocks + per8 - 1) / per8), lane::kThreads, 0, (hipStream_t) stream>>>(
+        x, rows, cols, xs, q, d);
+    return hipGetLastError() == hipSuccess;
+  }
+  const uint64_t per = lane::kThreads / 32;
   lane::round_kernel<<<(unsigned) ((blocks + per - 1) / per), lane::kThreads, 0, (hipStream_t) stream>>>(x, rows, cols,
                                                                                                         xs, q, d);
   return hipGetLastError() == hipSuccess;

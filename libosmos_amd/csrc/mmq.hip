@@ -57,6 +57,54 @@ __global__ __launch_bounds__(256) void x8_rows_kernel(const float* __restrict__ 
   }
 }
 
+// the same with 4 lanes a group, 8 values a lane (two 16-byte loads of the token's row, one 8-byte store): for x rows
+// 16-aligned. each value's code and the group's dx / sx exactly as above (max and the integer sum in any order)
+__global__ __launch_bounds__(256) void x8_rows8_kernel(const float* __restrict__ x, uint32_t xs,
+                                                       const int32_t* __restrict__ idx, uint32_t slots, uint32_t cols,
+                                                       int8_t* __restrict__ x8, float* __restrict__ dx,
+                                                       float* __restrict__ sx) {
+  const uint32_t groups = cols / MMQ_GROUP;
+  const uint64_t gi = ((uint64_t) blockIdx.x * 256 + threadIdx.x) / 4, ng = (uint64_t) slots * groups;
+  const uint32_t c8 = 8 * (threadIdx.x % 4);
+  const uint64_t gc = gi < ng ? gi : ng - 1;  // (past the end: the last group again, nothing stored)
+  const uint32_t s = (uint32_t) (gc / groups), g = (uint32_t) (gc % groups);
+  const int32_t r = idx[s];
+  float v[8];
+  if (r >= 0) {
+    const float4* src = (const float4*) (x + (uint64_t) r * xs + (uint64_t) g * MMQ_GROUP + c8);
+    const float4 lo = src[0], hi = src[1];
+    v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w, v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) a = fmaxf(a, fabsf(v[i]));
+  a = fmaxf(a, __shfl_xor(a, 1, 4));
+  a = fmaxf(a, __shfl_xor(a, 2, 4));
+  const float dd = __fdiv_rn(a, 127.0f);
+  int sum = 0;
+  uint64_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int qv = a == 0.0f ? 0 : (int) fminf(fmaxf(rintf(__fdiv_rn(v[i], dd)), -127.0f), 127.0f);
+    sum += qv;
+    w |= (uint64_t) (uint8_t) (int8_t) qv << (8 * i);
+  }
+  sum += __shfl_xor(sum, 1, 4);
+  sum += __shfl_xor(sum, 2, 4);
+  if (gi < ng) {
+    *(uint64_t*) (x8 + mmq_x8_at(s, g * MMQ_GROUP + c8, cols)) = w;
+    if (c8 == 0) {
+      const uint64_t at = mmq_dx_at(s, g, groups);
+      const float d0 = a == 0.0f ? 0.0f : dd;
+      dx[at] = d0;
+      sx[at] = __fmul_rn(d0, (float) sum);
+    }
+  }
+}
+
 // a workgroup: 64 rows (a wave 16) of matrix blockIdx.y over all of its cnt tokens, CT tiles of 16 at a time. each
 // wave keeps the 4 K partitions' sums side by side in registers (partition p the 256-blocks b with b % 4 == p, each
 // partition's groups in ascending order, then the 4 sums added in order - the contract's). a block's activations
@@ -220,6 +268,11 @@ extern "C" OSM_API bool mmq_x8_rows(const float* x, uint32_t xs, const int32_t* 
                                     int8_t* x8, float* dx, float* sx, void* stream) {
   if (!x || !idx || !x8 || !dx || !sx || !slots || !cols || cols % MMQ_GROUP || xs < cols) return false;
   const uint64_t work = (uint64_t) slots * cols;
+  if ((uintptr_t) x % 16 == 0 && xs % 4 == 0 && (uintptr_t) x8 % 8 == 0) {  // (the vector form where it is aligned)
+    mmq::x8_rows8_kernel<<<(unsigned) ((work / 8 + 255) / 256), 256, 0, (hipStream_t) stream>>>(x, xs, idx, slots, cols,
+                                                                                                x8, dx, sx);
+    return hipGetLastError() == hipSuccess;
+  }
   mmq::x8_rows_kernel<<<(unsigned) ((work + 255) / 256), 256, 0, (hipStream_t) stream>>>(x, xs, idx, slots, cols, x8,
                                                                                           dx, sx);
   return hipGetLastError() == hipSuccess;

@@ -56,6 +56,25 @@ def test_q8_round_random(g):
     assert (g.host(q) == qo).all() and (g.bits(g.host(d)) == g.bits(do)).all()
 
 
+def test_q8_round_unaligned(g):
+    """x rows not 16-aligned (an odd row stride, a start one float in): the one-value-a-lane form, the same bits"""
+    import torch
+    rng = np.random.default_rng(5)
+    rows, cols, xs = 9, 512, 517
+    x = (rng.normal(0, 1, (rows, cols)) * rng.uniform(0.01, 10, (rows, 1))).astype(np.float32)
+    buf = np.zeros(1 + rows * xs, np.float32)
+    for r in range(rows):
+        buf[1 + r * xs:1 + r * xs + cols] = x[r]
+    xd = g.dev(buf)
+    q = g.dev(np.zeros((rows, cols), np.int8))
+    d = g.dev(np.zeros((rows, cols // 32), np.float32))
+    from libosmos_amd import capi
+    assert capi.lib().q8_round(capi.ctypes.c_void_p(xd.data_ptr() + 4), rows, cols, xs, g.a(q), g.a(d), None)
+    torch.cuda.synchronize()
+    qo, do = orc.q8_round(x)
+    assert (g.host(q) == qo).all() and (g.bits(g.host(d)) == g.bits(do)).all()
+
+
 @pytest.mark.parametrize("name", REF_TYPES)
 def test_group_tok_golden(g, gold, name):
     """6 rows x 3 tokens of each shape: the reference cpu_q8_rows's bits"""

@@ -29,10 +29,11 @@ def x8_dev(g, x, idx, cols):
     return x8, dx, sx
 
 
-@pytest.mark.parametrize("cols", [2048, 7168])
-def test_x8_rows(g, cols):
+@pytest.mark.parametrize("cols,pad", [(2048, 32), (7168, 32), (2048, 1)])
+def test_x8_rows(g, cols, pad):
+    """the oracle's codes, dx and sx; a row stride of cols + 1 (rows not 16-aligned) takes the one-value-a-lane form"""
     rng = np.random.default_rng(4)
-    x = rng.normal(0, 1, (9, cols + 32)).astype(np.float32)
+    x = rng.normal(0, 1, (9, cols + pad)).astype(np.float32)
     x[3, 96:128] = 0
     idx = [0, 3, -1, 8, 2, 3, 7]
     x8, dx, sx = x8_dev(g, x, idx, cols)
