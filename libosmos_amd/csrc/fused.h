@@ -695,21 +695,21 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
 // are the picks of e (at most one a token), NB a pass: their x rows rounded into LDS, then each lane decodes its blocks
 // once and runs its chain links for every token of the pass (a chain accumulator a token), the trees, and
 // lane_swiglu(gate, up, lim, w[pick]) into h[pick][row] for each.
-template <uint32_t T, int L, int NB>
+template <uint32_t T, int L, int NB, int W = 4>  // W: the workgroup's waves, a row each
 struct GbLds {
   static constexpr uint32_t D = G1Max<L>::dim;
   static constexpr uint32_t grid = 0, q = align16(grid_bytes<T>()), d = q + NB * D, w = d + NB * (D / 32) * 4;
-  static constexpr uint32_t toks = w + align16(2 * kG1Rows * (uint32_t) row_bytes<T>(D));
-  static constexpr uint32_t ids = toks + align16((kMaxTok + 1) * 4);  // the routing ids of the first 2 kG1Threads picks
-  static constexpr uint32_t total = ids + 2 * kG1Threads * 4;
+  static constexpr uint32_t toks = w + align16(2 * (uint32_t) W * (uint32_t) row_bytes<T>(D));
+  static constexpr uint32_t ids = toks + align16((kMaxTok + 1) * 4);  // the routing ids of the first 2 (kWave * W) picks
+  static constexpr uint32_t total = ids + 2 * (kWave * W) * 4;
 };
 
 // one pass of gub_kernel: tokens toks[c0 .. c0 + live) (live <= NB), x rows from..NB-1 rounded into q/d (the rows
 // before from are there already), chains, trees and h
-template <uint32_t T, int L, int NB, bool P>
+template <uint32_t T, int L, int NB, bool P, int W>
 __device__ __forceinline__ void gub_pass(const GuArgs& a, const int32_t* toks, int c0, int live, int from, int8_t* q,
                                          float* d, const typename GridOf<T>::E* grid, const uint8_t* wr, uint32_t r0) {
-  constexpr int kThreads = kG1Threads;
+  constexpr int kThreads = (kWave * W);
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   const uint32_t nblk = a.dim / 32, lane = threadIdx.x % kWave, row = threadIdx.x / kWave;
   // the pass's x rows rounded (q8_round's bits): block b nblk + s is token b's block s (the rows past the live ones
@@ -799,15 +799,15 @@ __device__ __forceinline__ void gub_pass(const GuArgs& a, const int32_t* toks, i
   }
 }
 
-template <uint32_t T, int S, int L, int NB, bool P = false>
-__global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
-  using LD = GbLds<T, L, NB>;
+template <uint32_t T, int S, int L, int NB, bool P = false, int W = 4>
+__global__ __launch_bounds__(kWave * W) void gub_kernel(GuArgs a) {
+  using LD = GbLds<T, L, NB, W>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
-  constexpr int kThreads = kG1Threads;
-  constexpr uint32_t R = LD::D / 32 / (kThreads / 4);  // rounds that round a row of the largest dim
-  const uint32_t m = blockIdx.y, r0 = blockIdx.x * kG1Rows, n = a.n_tok * a.k;
+  constexpr int kThreads = (kWave * W);
+  constexpr uint32_t R = LD::D / 32 / (kThreads / 4) > 0 ? LD::D / 32 / (kThreads / 4) : 1;  // rounds for a row
+  const uint32_t m = blockIdx.y, r0 = blockIdx.x * (uint32_t) W, n = a.n_tok * a.k;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
-  const uint32_t per_seg = kG1Rows * rb / 16;
+  const uint32_t per_seg = (uint32_t) W * rb / 16;
   uint32_t idx[S];
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) idx[u] = min(u * kThreads + threadIdx.x, per_seg - 1);
@@ -883,23 +883,23 @@ __global__ __launch_bounds__(kG1Threads) void gub_kernel(GuArgs a) {
   const int cnt = __builtin_amdgcn_readfirstlane(toks[kMaxTok]);
   const auto* grid = (const typename GridOf<T>::E*) (smem + LD::grid);
   const uint32_t lane = threadIdx.x % kWave, row = threadIdx.x / kWave;
-  const uint8_t* wr = smem + LD::w + ((lane / 32) * kG1Rows + row) * rb;
+  const uint8_t* wr = smem + LD::w + ((lane / 32) * (uint32_t) W + row) * rb;
   // the first pass holds the owner's row already; full passes while NB tokens are left, then a token a pass
   int c0 = 0;
   if (cnt >= NB) {
-    gub_pass<T, L, NB, P>(a, toks, 0, NB, 1, q, d, grid, wr, r0);
+    gub_pass<T, L, NB, P, W>(a, toks, 0, NB, 1, q, d, grid, wr, r0);
     c0 = NB;
   } else {
-    gub_pass<T, L, 1, P>(a, toks, 0, 1, 1, q, d, grid, wr, r0);
+    gub_pass<T, L, 1, P, W>(a, toks, 0, 1, 1, q, d, grid, wr, r0);
     c0 = 1;
   }
   for (; c0 + NB <= cnt; c0 += NB) {
     __syncthreads();  // (the previous pass's codes read)
-    gub_pass<T, L, NB, P>(a, toks, c0, NB, 0, q, d, grid, wr, r0);
+    gub_pass<T, L, NB, P, W>(a, toks, c0, NB, 0, q, d, grid, wr, r0);
   }
   for (; c0 < cnt; c0++) {
     __syncthreads();
-    gub_pass<T, L, 1, P>(a, toks, c0, 1, 0, q, d, grid, wr, r0);
+    gub_pass<T, L, 1, P, W>(a, toks, c0, 1, 0, q, d, grid, wr, r0);
   }
 }
 

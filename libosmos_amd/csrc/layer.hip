@@ -58,26 +58,29 @@ bool gu1_launch_l(const GuArgs& a, hipStream_t s) {
 template <uint32_t T, int L>
 bool gub_launch_l(const GuArgs& a, hipStream_t s) {
   constexpr int NB = L == 16 ? 4 : 2;
-  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), words = fused::kG1Rows * rb / 16;
-  const dim3 grid(a.ff / fused::kG1Rows, a.n_tok * a.k);
-  constexpr int kT = fused::kG1Threads;
-  {  // (x already rounded: the P kernels copy it)
-    if (a.xq) {
-      if (words <= (uint32_t) kT)
-        fused::gub_kernel<T, 1, L, NB, true><<<grid, kT, 0, s>>>(a);
-      else if (words <= 2u * kT)
-        fused::gub_kernel<T, 2, L, NB, true><<<grid, kT, 0, s>>>(a);
-      else
-        fused::gub_kernel<T, fused::kG1Slots, L, NB, true><<<grid, kT, 0, s>>>(a);
-      return hipGetLastError() == hipSuccess;
-    }
+  // the workgroup's waves, a row each: 8 where the tile's fixed costs (its codebook table, its tokens' x, the routing
+  // ids) over twice the rows pay - 16 lanes (Qwen layer batch 4: 34.8 -> 30.9 us), and 32 lanes with a codebook of
+  // 8 KB or more (IQ1_S at DeepSeek batch 4: 160 -> 151 us); else 4 (at 32 lanes with a small codebook, 8 rows'
+  // LDS costs more occupancy than it saves: IQ2_XXS 224 -> 237 us). 16 was slower everywhere it fits
+  constexpr int W = L == 16 || fused::grid_bytes<T>() >= 8192 ? 8 : 4;
+  constexpr int kT = kWave * W;
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), words = W * rb / 16;
+  const dim3 grid(a.ff / W, a.n_tok * a.k);
+  if (a.xq) {  // (x already rounded: the P kernels copy it)
+    if (words <= (uint32_t) kT)
+      fused::gub_kernel<T, 1, L, NB, true, W><<<grid, kT, 0, s>>>(a);
+    else if (words <= 2u * kT)
+      fused::gub_kernel<T, 2, L, NB, true, W><<<grid, kT, 0, s>>>(a);
+    else
+      fused::gub_kernel<T, fused::kG1Slots, L, NB, true, W><<<grid, kT, 0, s>>>(a);
+    return hipGetLastError() == hipSuccess;
   }
   if (words <= (uint32_t) kT)
-    fused::gub_kernel<T, 1, L, NB><<<grid, kT, 0, s>>>(a);
+    fused::gub_kernel<T, 1, L, NB, false, W><<<grid, kT, 0, s>>>(a);
   else if (words <= 2u * kT)
-    fused::gub_kernel<T, 2, L, NB><<<grid, kT, 0, s>>>(a);
+    fused::gub_kernel<T, 2, L, NB, false, W><<<grid, kT, 0, s>>>(a);
   else
-    fused::gub_kernel<T, fused::kG1Slots, L, NB><<<grid, kT, 0, s>>>(a);
+    fused::gub_kernel<T, fused::kG1Slots, L, NB, false, W><<<grid, kT, 0, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
