@@ -231,8 +231,9 @@ bool launch(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
 }
 
 template <uint32_t T>
-bool fits(uint32_t rows, uint32_t cols) {
-  return rows && cols && rows % kTile == 0 && cols % Block<T>::values == 0 && cols % kStep == 0;
+bool fits(uint32_t rows, uint32_t cols) {  // (a matrix under 4 GB: the staging's 32-bit offsets)
+  return rows && cols && rows % kTile == 0 && cols % Block<T>::values == 0 && cols % kStep == 0 &&
+         (uint64_t) rows * row_bytes<T>(cols) <= 0xFFFFFFFFull;
 }
 
 template <uint32_t T>
