@@ -33,9 +33,12 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   constexpr int G = kWave / L, per = (int) (Block<T>::values / 32);
   const int lane = threadIdx.x % kWave, ll = lane % L;
   const uint32_t m = blockIdx.y, row = (blockIdx.x * kWaves + threadIdx.x / kWave) * G + lane / L;
-  const uint32_t n = (uint32_t) cnt[m];
-  if (!n) return;  // an entry past a device-built table's live ones (osmos_lane_tables): nothing read or written
-  const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m];
+  // (blockIdx.z: the matrix's token tile, tokens z NT .. z NT + NT - 1 of its cnt[m])
+  const uint32_t n_all = (uint32_t) cnt[m], z0 = blockIdx.z * NT;
+  if (n_all <= z0) return;  // an entry past a device-built table's live ones (osmos_lane_tables), or a tile past its
+                            // tokens: nothing read or written
+  const uint32_t n = n_all - z0 < (uint32_t) NT ? n_all - z0 : NT;
+  const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m] + z0;
   const uint8_t* rb = w[m] + (uint64_t) (row < rows ? row : 0) * row_bytes<T>(cols);
   uint64_t xr[NT];
   in_rows<NT>(xin, r0, n, xr);
@@ -75,9 +78,10 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(const uint8_t* const*
   constexpr int G = kWave / L, per = (int) (Block<T>::values / 32);
   const int lane = threadIdx.x % kWave, ll = lane % L;
   const uint32_t m = blockIdx.y, row = (blockIdx.x * kWaves + threadIdx.x / kWave) * G + lane / L;
-  const uint32_t n = (uint32_t) cnt[m];
-  if (!n) return;  // as group_tok_kernel
-  const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m];
+  const uint32_t n_all = (uint32_t) cnt[m], z0 = blockIdx.z * NT;
+  if (n_all <= z0) return;  // as group_tok_kernel
+  const uint32_t n = n_all - z0 < (uint32_t) NT ? n_all - z0 : NT;
+  const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m] + z0;
   const uint64_t off = (uint64_t) (row < rows ? row : 0) * row_bytes<T>(cols);
   const uint8_t *rg = wg[m] + off, *ru = wu[m] + off;
   uint64_t xr[NT];
@@ -166,9 +170,9 @@ struct Args {
 };
 
 template <uint32_t T, int NT, int L>
-bool launch(const Args& a, bool fused, hipStream_t s) {
+bool launch(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
   constexpr uint32_t per_block = kWaves * (kWave / L);
-  const dim3 grid((a.rows + per_block - 1) / per_block, a.n);
+  const dim3 grid((a.rows + per_block - 1) / per_block, a.n, tiles);
   if (fused)
     gate_up_kernel<T, NT, L><<<grid, kThreads, 0, s>>>((const uint8_t* const*) a.wg, (const uint8_t* const*) a.wu,
                                                          a.cnt, a.xrow, a.xin, a.win, a.rows, a.cols, a.q, a.d,
@@ -180,8 +184,8 @@ bool launch(const Args& a, bool fused, hipStream_t s) {
 }
 
 template <uint32_t T, int NT>
-bool by_lanes(const Args& a, bool fused, hipStream_t s) {
-  return a.cols >= 4096 ? launch<T, NT, 32>(a, fused, s) : launch<T, NT, 16>(a, fused, s);
+bool by_lanes(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
+  return a.cols >= 4096 ? launch<T, NT, 32>(a, fused, s, tiles) : launch<T, NT, 16>(a, fused, s, tiles);
 }
 
 template <uint32_t T>
@@ -192,10 +196,9 @@ bool by_tokens(const Args& a, uint32_t max_cnt, bool fused, hipStream_t s) {
     case 2: return by_lanes<T, 2>(a, fused, s);
     case 3: return by_lanes<T, 3>(a, fused, s);
     case 4: return by_lanes<T, 4>(a, fused, s);
-    case 5: return by_lanes<T, 5>(a, fused, s);
-    case 6: return by_lanes<T, 6>(a, fused, s);
-    case 7: return by_lanes<T, 7>(a, fused, s);
-    case 8: return by_lanes<T, 8>(a, fused, s);
+    // (5 to 8 tokens: two tiles of 4 - twice the waves for the matrix, each with half the tokens' sums a block; every
+    // token's chain the same)
+    case 5: case 6: case 7: case 8: return by_lanes<T, 4>(a, fused, s, 2);
     default: return false;
   }
 }
