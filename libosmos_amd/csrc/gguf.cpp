@@ -130,12 +130,14 @@ class Cursor {
   bool value(GgufKv& kv) {
     uint32_t t = 0;
     if (!u32(&t)) return false;
+    if (t > GGUF_FLOAT64) return fail("an unknown value type");  // (checked before it is stored as the enum)
     kv.type = (GgufValueType) t;
     if (t == GGUF_STRING) return (kv.v.s = str()) != nullptr;
     if (t != GGUF_ARRAY) return scalar(t, kv);
     uint32_t item = 0;
     uint64_t n = 0;
     if (!u32(&item) || !u64(&n)) return false;
+    if (item > GGUF_FLOAT64) return fail("an array of an unknown value type");
     kv.item = (GgufValueType) item;
     if (item == GGUF_STRING) {
       if (n > left() / 8) return fail("an array longer than the file");  // (each string at least its length)

@@ -155,6 +155,7 @@ def test_corrupt(tmp_path):
     # an unknown value type (13), an array of one, a string past the end, counts past the file
     head = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + W.s("k")
     for tail in (struct.pack("<I", 13) + b"\0" * 8, struct.pack("<IIQ", 9, 13, 1) + b"\0" * 8,
+                 struct.pack("<I", 0x61737961) + b"\0" * 8, struct.pack("<IIQ", 9, 0x61737961, 1) + b"\0" * 8,
                  struct.pack("<IQ", 8, 1 << 40), struct.pack("<IIQ", 9, 4, 1 << 40)):
         refused(write(tmp_path, "v.gguf", head + tail + b"\0" * 32))
     refused(write(tmp_path, "n.gguf", b"GGUF" + struct.pack("<IQQ", 3, 1 << 50, 0) + b"\0" * 64))
