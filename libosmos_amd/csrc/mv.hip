@@ -22,7 +22,15 @@ constexpr int kWaves = 4, kThreads = kWave * kWaves, kHalf = 32;
 
 // R rows of one half-wave over NT tokens: x rows xs floats apart (token t's at x + t xs), y's ys apart; rows past
 // `rows` decode row 0 and store nothing; tokens at or past `live` read the last live token and store nothing
-template <uint32_t T, int NT, int R>
+// STG (one row a half-wave, the row a whole number of 16-byte words, at most kStgMax bytes, the matrix 16-aligned): the
+// half-wave first copies its row into its own LDS slot with 16-byte loads (a row's bytes in a few wide loads rather
+// than a few bytes a chunk), then decodes the same bytes from there - the same values, so the same bits
+constexpr uint32_t kStgMax = 2048;
+// the types whose decode reads a chunk's bytes in many small pieces (Q4_K / Q5_K's 6-bit scale pairs, IQ1's
+// scattered fields); measured on 8192 x 2048 at one token, staged / not (us): Q4_K 11.0 / 14.8, Q5_K 14.0 / 23.6,
+// IQ1_M 8.1 / 9.1, IQ1_S 7.9 / 8.2; Q4_0, Q2_K, Q3_K, Q6_K, IQ3_XXS and IQ4_XS were 5-20 % slower staged
+template <uint32_t T> constexpr bool stages() { return T == kQ4_K || T == kQ5_K || T == kIQ1_M || T == kIQ1_S; }
+template <uint32_t T, int NT, int R, bool STG = false>
 __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* __restrict__ x,
                                uint32_t xs, float* __restrict__ y, uint32_t ys, uint32_t live) {
   const int lane = threadIdx.x % kHalf;
@@ -31,6 +39,24 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
   const uint8_t* base[R];
 #pragma unroll
   for (int q = 0; q < R; q++) base[q] = w + (uint64_t) (row0 + q < rows ? row0 + q : 0) * row_bytes<T>(cols);
+  if constexpr (STG) {
+    static_assert(R == 1, "a staged half-wave holds one row");
+    __shared__ __attribute__((aligned(16))) uint8_t stg[2 * kWaves][kStgMax];
+    uint8_t* slot = stg[threadIdx.x / kHalf];
+    const uint32_t words = (uint32_t) row_bytes<T>(cols) / 16;
+    const uint4* src = (const uint4*) base[0];
+    uint4 r[kStgMax / 16 / kHalf];
+#pragma unroll
+    for (int i = 0; i < (int) (kStgMax / 16 / kHalf); i++)
+      if (lane + i * kHalf < (int) words) r[i] = src[lane + i * kHalf];
+#pragma unroll
+    for (int i = 0; i < (int) (kStgMax / 16 / kHalf); i++)
+      if (lane + i * kHalf < (int) words) ((uint4*) slot)[lane + i * kHalf] = r[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // (the slot is the half-wave's own: no workgroup barrier)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    base[0] = slot;
+  }
   const float* xt[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) xt[t] = x + (uint64_t) ((uint32_t) t < live ? t : live - 1) * xs;
@@ -76,12 +102,12 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
 }
 
 // one matrix, n_tok tokens in tiles of NT over blockIdx.y
-template <uint32_t T, int NT, int R>
+template <uint32_t T, int NT, int R, bool STG = false>
 __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols,
                                                    const float* __restrict__ x, uint32_t xs, uint32_t n_tok,
                                                    float* __restrict__ y, uint32_t ys) {
   const uint32_t t0 = blockIdx.y * NT, live = n_tok - t0 < (uint32_t) NT ? n_tok - t0 : NT;
-  rows_of<T, NT, R>(w, rows, cols, x + (uint64_t) t0 * xs, xs, y + (uint64_t) t0 * ys, ys, live);
+  rows_of<T, NT, R, STG>(w, rows, cols, x + (uint64_t) t0 * xs, xs, y + (uint64_t) t0 * ys, ys, live);
 }
 
 // n matrices of one shape (blockIdx.y the matrix): x at x + (m / x_div) x_mat, y at y + m rows
@@ -114,7 +140,11 @@ bool run_nt(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_
             uint32_t ys, hipStream_t s) {
   constexpr uint32_t per = kWaves * 2 * rows_per<NT>();
   const dim3 grid((rows + per - 1) / per, (n_tok + NT - 1) / NT);
-  kernel<T, NT, rows_per<NT>()><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+  const uint32_t rb = (uint32_t) row_bytes<T>(cols);
+  if (stages<T>() && NT == 1 && rb % 16 == 0 && rb <= kStgMax && (uintptr_t) w % 16 == 0)
+    kernel<T, NT, rows_per<NT>(), NT == 1><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+  else
+    kernel<T, NT, rows_per<NT>()><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
   return hipGetLastError() == hipSuccess;
 }
 
