@@ -121,3 +121,27 @@ def test_refusals(g):
     assert not L.mv_group(2, p, 0, 16, 512, p, 0, 1, p, None) and not L.mv_group(2, p, 2, 16, 512, p, 0, 0, p, None)
     assert not L.mv_group_tok(2, p, p, p, 1, 9, 16, 512, p, 512, p, 16, None)
     assert not L.quant_known(99) and L.quant_known(18)
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "IQ1_M"])
+def test_mv_one_token_unaligned_matrix(g, name):
+    """one token, a matrix whose start is 8- but not 16-byte aligned: the launch keeps the direct path (the staged
+    path copies rows with 16-byte loads and takes only 16-aligned matrices) - the oracle's bits, the same as the
+    aligned copy's"""
+    import torch
+    t = synth.ID[name]
+    rows, cols = 70, 2048
+    w = weights(name, rows, cols, 9)
+    n = w.size
+    buf = torch.zeros(n + 64, dtype=torch.uint8, device="cuda")
+    buf[8:8 + n] = torch.from_numpy(np.ascontiguousarray(w).reshape(-1)).cuda()
+    wa = g.dev(w)
+    x = np.random.default_rng(4).normal(0, 1, (1, cols)).astype(np.float32)
+    want = orc.mv_rows(t, w, rows, cols, x)
+    xd = g.dev(x)
+    for wt, what in ((buf[8:8 + n], "offset 8"), (wa, "aligned")):
+        assert wt.data_ptr() % 16 == (8 if what == "offset 8" else 0)
+        y = torch.full((1, rows), float("nan"), device="cuda")
+        print("mv_run one token", name, what, flush=True)
+        g.call("mv_run", t, g.a(wt), rows, cols, g.a(xd), 1, g.a(y), None)
+        assert (g.bits(g.host(y)) == g.bits(want)).all(), what
