@@ -116,7 +116,16 @@ __global__ __launch_bounds__(kThreads) void group_kernel(const uint8_t* const* _
                                                          uint32_t cols, const float* __restrict__ x, uint32_t x_mat,
                                                          uint32_t x_div, float* __restrict__ y) {
   const uint32_t m = blockIdx.y;
-  rows_of<T, 1, R>(w[m], rows, cols, x + (uint64_t) (m / x_div) * x_mat, cols, y + (uint64_t) m * rows, rows, 1);
+  const uint8_t* wm = w[m];
+  const float* xm = x + (uint64_t) (m / x_div) * x_mat;
+  if constexpr (stages<T>() && R == 1) {  // (the matrix's alignment is known only here: a uniform choice per matrix)
+    const uint32_t rb = (uint32_t) row_bytes<T>(cols);
+    if (rb % 16 == 0 && rb <= kStgMax && (uintptr_t) wm % 16 == 0) {
+      rows_of<T, 1, R, true>(wm, rows, cols, xm, cols, y + (uint64_t) m * rows, rows, 1);
+      return;
+    }
+  }
+  rows_of<T, 1, R>(wm, rows, cols, xm, cols, y + (uint64_t) m * rows, rows, 1);
 }
 
 // matrices each over their own cnt[m] tokens from row xrow[m] (0: skipped)
