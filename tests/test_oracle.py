@@ -284,3 +284,172 @@ def test_mmq_bound_and_quantization():
         terms = (wa * qx * dxs) - (wc * qx * dxs)
         exact = terms.sum(axis=1)
         assert np.all(np.abs(y - exact) <= (cols // 32 + 8) * 2.0 ** -23 * np.abs(terms).sum(axis=1) + 1e-30)
+
+
+# ---- the mmq contract's order, bit for bit, from exactly rounded float32 operations ----
+
+def b32(v):
+    return int(np.float32(v).view(np.uint32))
+
+
+def _mmq_exact(blocks, x8s, dxs, sxs, variant=""):
+    """one Q4_K row (blocks [nb, 144]) against one slot's codes x8s [cols], scales dxs / sxs [groups], in the order
+    reference include/osmos/gpu/mmq.h:37-55 and tests/gpu/test_mmq_gpu.hip:94-115 state: partition p takes blocks
+    p, p + 4, ...; per group v = (d sc) dx, acc = fma(v, I, acc), acc = fma(dmin m, -sx, acc); then
+    ((p0 + p1) + p2) + p3. Every float step is a correctly rounded binary32 operation (tests/exact32.py).
+    variant: "muladd" (a product then a sum in place of each fma), "reverse" (the partitions summed 3 .. 0) or
+    "serial" (one chain over all blocks): orders the contract rules out, used to show the test can see them."""
+    import exact32 as e
+    nb = blocks.shape[0]
+    d, dmin = refdecode._h(blocks, 0), refdecode._h(blocks, 2)
+    sc, mn = refdecode._k_scales(blocks[:, 4:16].astype(np.int64))
+    parts = [np.float32(0.0)] * 4
+    order = [(p, b) for p in range(4) for b in range(p, nb, 4)] if variant != "serial" else [(0, b) for b in range(nb)]
+    for p, b in order:
+        for g in range(8):
+            q = ((blocks[b, 16 + 32 * (g // 2):16 + 32 * (g // 2) + 32].astype(np.int64) >> (4 * (g % 2))) & 15)
+            gg = 8 * b + g
+            isum = int((q * x8s[32 * gg:32 * gg + 32].astype(np.int64)).sum())
+            dsc = e.mul(np.float32(d[b]), np.float32(sc[b, g]))
+            dm = e.mul(np.float32(dmin[b]), np.float32(mn[b, g]))
+            v = e.mul(dsc, dxs[gg])
+            if variant == "muladd":
+                parts[p] = e.add(e.mul(v, np.float32(isum)), parts[p])
+                parts[p] = e.add(e.mul(dm, -sxs[gg]), parts[p])
+            else:
+                parts[p] = e.fma(v, np.float32(isum), parts[p])
+                parts[p] = e.fma(dm, -sxs[gg], parts[p])
+    seq = [3, 2, 1, 0] if variant == "reverse" else [0, 1, 2, 3]
+    r = parts[seq[0]]
+    for p in seq[1:]:
+        r = e.add(r, parts[p])
+    return r
+
+
+@pytest.mark.parametrize("cols", [1024, 2048])
+def test_mmq_rows_exact_order(cols):
+    """orc_mmq_rows equals, bit for bit, the contract's operations replayed in exactly rounded binary32; a product and a
+    sum in place of an fma, the partitions summed in reverse, or one serial chain each change some row's bits on the
+    same inputs (so the check sees those mistakes)"""
+    rng = np.random.default_rng(23 + cols)
+    rows = 12
+    w = synth.random_blocks(synth.ID["Q4_K"], rows, cols, 5 + cols)
+    x = rng.normal(0, 1, (3, cols)).astype(np.float32)
+    idx = np.array([2, 0, 1], np.int32)
+    x8, dx, sx = orc.mmq_x8_rows(x, idx, cols)
+    L = orc.orc()
+    blocks = w.reshape(rows, cols // 256, 144)
+    differs = {"muladd": 0, "reverse": 0, "serial": 0}
+    for s in range(len(idx)):
+        y = orc.mmq_rows(w, rows, cols, x8, dx, sx, s)
+        x8s = np.array([x8[L.orc_mmq_x8_at(s, i, cols)] for i in range(cols)], np.int8)
+        at = [L.orc_mmq_dx_at(s, g, cols // 32) for g in range(cols // 32)]
+        dxs, sxs = dx[at], sx[at]
+        for r in range(rows):
+            want = _mmq_exact(blocks[r], x8s, dxs, sxs)
+            assert b32(y[r]) == b32(want), (s, r, y[r], want)
+            for v in differs:
+                differs[v] += int(b32(_mmq_exact(blocks[r], x8s, dxs, sxs, v)) != b32(want))
+    assert all(n > 0 for n in differs.values()), differs
+
+
+def test_mmq_rows_one_block_closed_form():
+    """a row whose only nonzero block is block p (of 4: partition p alone, one block) over one group: the result is
+    fma(dmin m, -sx, fma((d sc) dx, I, 0)) exactly, whichever partition holds it"""
+    import exact32 as e
+    cols = 1024
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    x8, dx, sx = orc.mmq_x8_rows(x, np.array([0], np.int32), cols)
+    L = orc.orc()
+    for p in range(4):
+        blk = np.zeros((4, 144), np.uint8)
+        blk[p, 0:2] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+        blk[p, 2:4] = np.frombuffer(np.float16(0.0071).tobytes(), np.uint8)
+        blk[p, 4] = 37  # group 0: sc 37, m 21
+        blk[p, 8] = 21
+        blk[p, 16:48] = rng.integers(0, 16, 32)
+        y = orc.mmq_rows(blk.reshape(-1), 1, cols, x8, dx, sx, 0)
+        gg = 8 * p
+        at = L.orc_mmq_dx_at(0, gg, cols // 32)
+        q = blk[p, 16:48].astype(np.int64) & 15
+        xs = np.array([x8[L.orc_mmq_x8_at(0, 32 * gg + i, cols)] for i in range(32)], np.int64)
+        dsc = e.mul(np.float16(0.0123).astype(np.float32), np.float32(37))
+        dm = e.mul(np.float16(0.0071).astype(np.float32), np.float32(21))
+        want = e.fma(dm, -sx[at], e.fma(e.mul(dsc, dx[at]), np.float32((q * xs).sum()), np.float32(0)))
+        assert b32(y[0]) == b32(want), p
+
+
+# ---- the MoE plumbing against float64 ----
+
+def _route64(logits, k):
+    """float64 softmax, the k most probable (the greater first, the lower id among equals), weights p / max(sum, floor)
+    (reference include/osmos/gpu/q4x_ops.h:356-360)"""
+    l = logits.astype(np.float64)
+    p = np.exp(l - l.max())
+    p /= p.sum()
+    order = sorted(range(len(p)), key=lambda i: (-p[i], i))[:k]
+    pk = p[order]
+    return np.array(order), pk / max(pk.sum(), 6.103515625e-5)
+
+
+def test_route_float64():
+    """orc_route's ids are float64's top-k (ties: the lower id, also among exactly equal logits), its weights within a
+    few ulp of float64's; well-separated logits so float32 rounding cannot reorder the picks"""
+    rng = np.random.default_rng(31)
+    for n_tok, n_exp, k in [(5, 512, 10), (4, 256, 8), (3, 64, 1), (2, 1024, 32)]:
+        base = rng.permutation(n_exp).astype(np.float32) * np.float32(0.01)  # distinct, 0.01 apart
+        logits = np.stack([np.roll(base, 7 * t) for t in range(n_tok)]).astype(np.float32)
+        logits[0, 3] = logits[0, 9] = logits[0].max()  # an exact tie at the top: 3 first, then 9
+        ids = np.zeros((n_tok, k), np.int32)
+        w = np.zeros((n_tok, k), np.float32)
+        orc.orc().orc_route(orc.ptr(logits), n_tok, n_exp, k, orc.ptr(ids), orc.ptr(w))
+        for t in range(n_tok):
+            i64, w64 = _route64(logits[t], k)
+            assert (ids[t] == i64).all(), (n_tok, n_exp, k, t)
+            assert np.all(np.abs(w[t] - w64) <= 8 * 2.0 ** -24 * w64), (n_tok, n_exp, k, t)
+        if k > 1:
+            assert ids[0, 0] == 3 and ids[0, 1] == 9 and w[0, 0] == w[0, 1]
+
+
+def test_route_sum_floor():
+    """the weights' divisor is max(sum of the k probabilities, 6.103515625e-5): with 20000 equal logits and k = 1 the
+    sum is 5e-5, under the floor, so w = (1/20000) / 6.103515625e-5 = 0.8192 - and k = 2 (1e-4, over it) gives 0.5"""
+    n = 20000
+    logits = np.zeros((1, n), np.float32)
+    for k, want in [(1, 0.8192), (2, 0.5)]:
+        ids = np.zeros(k, np.int32)
+        w = np.zeros(k, np.float32)
+        orc.orc().orc_route(orc.ptr(logits), 1, n, k, orc.ptr(ids), orc.ptr(w))
+        assert list(ids) == list(range(k))
+        assert abs(float(w[0]) - want) <= 1e-6 * want, (k, w)
+
+
+def test_moe_sum_float64():
+    """orc_moe_sum: out[t] = sum over j in order of y[where[t k + j]] w[t k + j], plus shared[t] sigmoid(logit[t]):
+    exact where every term is (small integers, power-of-two weights; logit 0 gives 1/2, a large logit 1 and a very
+    negative one 0); within (k + 2) ulp-sums of float64 on random inputs"""
+    rng = np.random.default_rng(41)
+    n_tok, k, dim, n_rows = 4, 3, 64, 9
+    y = rng.integers(-50, 50, (n_rows, dim)).astype(np.float32)
+    where = rng.permutation(n_tok * k).astype(np.int32) % n_rows
+    w = np.float32(2.0) ** rng.integers(-3, 3, n_tok * k).astype(np.float32)
+    sh = rng.integers(-50, 50, (n_tok, dim)).astype(np.float32)
+    sl = np.array([0.0, 100.0, -200.0, 0.0], np.float32)
+    out = np.zeros((n_tok, dim), np.float32)
+    orc.orc().orc_moe_sum(orc.ptr(y), orc.ptr(where), orc.ptr(w), n_tok, k, dim, orc.ptr(sh), orc.ptr(sl), orc.ptr(out))
+    gate = np.array([0.5, 1.0, 0.0, 0.5])
+    want = np.stack([sum(y[where[t * k + j]].astype(np.float64) * w[t * k + j] for j in range(k)) + sh[t] * gate[t]
+                     for t in range(n_tok)])
+    assert (out == want).all()
+    # random: the float32 sum against float64
+    y = rng.normal(0, 1, (n_rows, dim)).astype(np.float32)
+    w = rng.uniform(0, 1, n_tok * k).astype(np.float32)
+    sl = rng.normal(0, 2, n_tok).astype(np.float32)
+    orc.orc().orc_moe_sum(orc.ptr(y), orc.ptr(where), orc.ptr(w), n_tok, k, dim, orc.ptr(sh), orc.ptr(sl), orc.ptr(out))
+    for t in range(n_tok):
+        g64 = 1.0 / (1.0 + np.exp(-np.float64(sl[t])))
+        terms = [y[where[t * k + j]].astype(np.float64) * w[t * k + j] for j in range(k)] + [sh[t] * g64]
+        exact = sum(terms)
+        mag = sum(np.abs(a) for a in terms)
+        assert np.all(np.abs(out[t] - exact) <= (k + 4) * 2.0 ** -24 * mag + 1e-30), t
