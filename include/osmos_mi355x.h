@@ -49,6 +49,16 @@ uint64_t osmos_lane_workspace(const OsmosLaneLayer *layer, uint32_t n_tok);
 bool osmos_lane_layer(const OsmosLaneLayer *layer, const float *x, uint32_t n_tok, const int32_t *ids, const float *w,
                       const float *add, float *out, void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* osmos_lane_layer with no workspace argument and no allocation, for callers that cannot allocate device memory (code
+   under HIP graph capture, serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. Its
+   workspace is a static device array of OSMOS_LANE_SCRATCH_BYTES a GPU inside this library (looked up once a device on
+   the first call there, held until the process ends): a layer whose osmos_lane_workspace(layer, n_tok) exceeds that is
+   refused (false, nothing queued). Every call on one GPU shares that GPU's array, so calls on one GPU must be ordered
+   (one stream, or synchronised): calls that overlap on one GPU race. The same bits as osmos_lane_layer. */
+#define OSMOS_LANE_SCRATCH_BYTES (16u << 20)
+bool osmos_lane_layer_noalloc(const OsmosLaneLayer *layer, const float *x, uint32_t n_tok, const int32_t *ids,
+                              const float *w, const float *add, float *out, void *stream);
+
 /* the lane contract at prefill scale: q8_group_tok's sums (include/osmos/gpu/q8.h; reference kernels/q8.h:178-212,
    src/cpu/q8.c:383-407) for any token count - matrix m (w[m], rows x cols of `type`) over rows xrow[m] ..
    xrow[m] + cnt[m] - 1 of the rounded activations q / d (q8_round's layout), into the same rows of y (ys apart); the

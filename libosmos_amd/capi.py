@@ -73,6 +73,7 @@ class Q4xExpertBounds(ctypes.Structure):
 SIGS.update({
     "osmos_lane_workspace": (U64, [ctypes.POINTER(OsmosLaneLayer), U32]),
     "osmos_lane_layer": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P, P, U64, P]),
+    "osmos_lane_layer_noalloc": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P, P]),
     "osmos_lane_gate_up": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P]),
     "osmos_lane_down": (B, [ctypes.POINTER(OsmosLaneLayer), P, U32, P, P, P, P]),
     "osmos_lane_group": (B, [U32, P, P, P, U32, U32, U32, U32, P, P, P, U32, P]),

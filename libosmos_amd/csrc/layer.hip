@@ -2,6 +2,8 @@
 // osmos_lane_workspace): two fused launches (fused.h) - gate/up with the activation, then down with the tokens'
 // ordered expert sums - in the order of the reference's src/run/hip_lane.c:115-222 and src/cpu/lane.c:98-118, so every
 // output is the reference CPU lane's bits. no host round trip, no allocation: capturable in a HIP graph.
+#include <mutex>
+
 #include "fused.h"
 
 extern "C" {
@@ -254,4 +256,43 @@ extern "C" OSM_API bool osmos_lane_layer(const OsmosLaneLayer* L, const float* x
   const fused::DnArgs da = {h, ids, n_tok, L->k, L->dim, L->ff, (const uint8_t*) L->down, L->down_bytes, add, out,
                             hq, hd};
   return layer::dn(L->type_down, da, s);
+}
+
+// ---- the layer with no allocation and no caller workspace: the workspace is this file's static device array ----
+namespace osm {
+namespace layer {
+
+// OSMOS_LANE_SCRATCH_BYTES of device memory, one copy a GPU, held until the process ends. Host code never uses the
+// symbol's name as an address: each device's copy is looked up once (hipGetSymbolAddress, that device current) and
+// that address is what the kernels get
+static __device__ __align__(256) uint8_t scratch[OSMOS_LANE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices];
+
+// the calling thread's current device's copy (nullptr: no device, or the lookup failed)
+void* scratch_here() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> g(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    scratch_dev[dev] = p;
+  }
+  return scratch_dev[dev];
+}
+
+}  // namespace layer
+}  // namespace osm
+
+extern "C" OSM_API bool osmos_lane_layer_noalloc(const OsmosLaneLayer* L, const float* x, uint32_t n_tok,
+                                                 const int32_t* ids, const float* w, const float* add, float* out,
+                                                 void* stream) {
+  const uint64_t need = osmos_lane_workspace(L, n_tok);  // (0 for a descriptor or count refused below)
+  if (!need || need > OSMOS_LANE_SCRATCH_BYTES) return false;
+  void* ws = layer::scratch_here();
+  if (!ws) return false;
+  return osmos_lane_layer(L, x, n_tok, ids, w, add, out, ws, need, stream);
 }
