@@ -317,21 +317,32 @@ def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=
     step_bytes = sum(distinct) / G * per_expert + n_tok * dim * 4 * 2 + n_tok * k * 8
 
     s = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        for st in range(G):  # one eager pass (also the warm-up of every code path)
-            layers[st % n_layers].forward(x[st], ids[st], w[st], add, out[st], stream=s.cuda_stream)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=s):
-            for st in range(G):
-                layers[st % n_layers].forward(x[st], ids[st], w[st], add, out[st], stream=s.cuda_stream)
+
+    def run(st):
+        layers[st % n_layers].forward(x[st % G], ids[st % G], w[st % G], add, out[st % G], stream=s.cuda_stream)
+
+    with torch.cuda.stream(s):  # exactly `warmup` untimed steps (eager: also the first use of every code path)
+        for st in range(warmup):
+            run(st)
     torch.cuda.synchronize()
-    reps = max(1, steps // G)
+    # the timed steps: exactly `steps`, as replays of a graph of min(steps, G) steps plus one graph of the remainder
+    per = min(steps, G)
+    graphs = []
+    for n in ([per] * (steps // per)) + ([steps % per] if steps % per else []):
+        if not graphs or n != per:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(graph, stream=s):
+                    for st in range(n):
+                        run(st)
+            graphs.append((graph, n))
+        else:
+            graphs.append(graphs[0])
+    torch.cuda.synchronize()
     ev = Events(torch)
-    for _ in range(max(1, warmup // G)):
-        graph.replay()
-    ms = ev.time(graph.replay, reps)
-    n_steps = reps * G
+    ms = ev.time(lambda: [g.replay() for g, _ in graphs], 1)
+    n_steps = sum(n for _, n in graphs)
+    assert n_steps == steps
     ms_step = ms / n_steps
     return dict(n_tok=n_tok, steps=n_steps, ms_per_step=ms_step, step_bytes=step_bytes,
                 gbs=step_bytes / (ms_step * 1e-3) / 1e9, layers=layers, ids=ids, w=w, x=x, G=G, n_layers=n_layers,
@@ -441,6 +452,54 @@ def cpu_baseline(lay, seconds=10.0):
                       % (reps, n_tok, len(experts), per * 1e3)}
 
 
+def ceilings(torch):
+    """the box's own ceilings for the roofline: a best-shaped streaming read (bench-calibration kernel calib_read: every
+    thread a run of 16-byte loads all in flight) of the layer kernels' byte counts and of large reads, each launch on
+    fresh bytes of a 4 GiB pool (beyond the 256 MB Infinity Cache), graph-launched like the bench; and chains of dense
+    MFMAs (int8 and f16) over 2048 workgroups: the matrix cores' measured peak"""
+    L = ctypes.CDLL(os.path.join(ROOT, "libosmos_amd", "libosmos_calib.so"))
+    L.calib_read.restype = ctypes.c_bool
+    L.calib_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64] + [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 2
+    L.calib_mfma.restype = ctypes.c_bool
+    L.calib_mfma.argtypes = [ctypes.c_uint32] * 3 + [ctypes.c_void_p] * 2
+    pool_bytes = 4 << 30
+    pool = torch.empty(pool_bytes, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    out = {"read": {}, "mfma": {}}
+    for nbytes in (4050944, 8056832, 12107776, 64 << 20, 1 << 30):
+        best = None
+        for threads, unroll in ((256, 4), (256, 8), (256, 16), (512, 8), (1024, 4), (1024, 8)):
+            for grid in (256, 512, 1024, 2048):
+                if grid * threads * unroll * 16 > nbytes * 2:
+                    continue
+                slots = max(1, pool_bytes // nbytes)
+                G = min(32, slots)
+
+                def launch(i, st, threads=threads, unroll=unroll, grid=grid):
+                    src = pool.data_ptr() + (i % slots) * (nbytes // 4096 * 4096)
+                    return L.calib_read(src, nbytes, grid, threads, unroll, sink.data_ptr(), st)
+                us = graph_us(torch, launch, G, reps=5)
+                if best is None or us < best[0]:
+                    best = (us, threads, unroll, grid)
+        us, threads, unroll, grid = best
+        out["read"][str(nbytes)] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                    "pct_hbm_peak": round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 1),
+                                    "threads": threads, "unroll": unroll, "workgroups": grid}
+        log("read %d B: %.2f us (%d threads x %d, %d workgroups)" % (nbytes, us, threads, unroll, grid))
+    empty = graph_us(torch, lambda i, st: L.calib_read(pool.data_ptr(), 16, 1, 256, 4, sink.data_ptr(), st), 32)
+    out["read"]["one_line_launch_us"] = round(empty, 3)
+    blocks, iters = 2048, 4000
+    for kind, name, mnk, peak in ((0, "int8_16x16x64", 16 * 16 * 64, INT8_PEAK_TOPS),
+                                  (1, "int8_32x32x32", 32 * 32 * 32, INT8_PEAK_TOPS),
+                                  (2, "f16_16x16x32", 16 * 16 * 32, F16_PEAK_TFLOPS),
+                                  (3, "f16_32x32x16", 32 * 32 * 16, F16_PEAK_TFLOPS)):
+        us = graph_us(torch, lambda i, st: L.calib_mfma(kind, blocks, iters, sink.data_ptr(), st), 4, reps=3)
+        t = 2.0 * mnk * blocks * 4 * iters * 4 / us / 1e6
+        out["mfma"][name] = {"us": round(us, 1), "T_per_s": round(t, 1), "pct_peak": round(100 * t / peak, 1)}
+        log("mfma %s: %.1f T/s (%.1f %% of %g)" % (name, t, 100 * t / peak, peak))
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -452,6 +511,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain device copy of 64 MiB, 8 times (the calibration kernel of a counter run)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="only the box's ceilings (streaming read, MFMA chains), one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (--gpus %d refused)" % args.gpus)
@@ -460,6 +521,9 @@ def main():
     from libosmos_amd import capi
     capi.lib()
     torch.cuda.set_device(0)
+    if args.ceilings:
+        print(json.dumps({"ceilings": ceilings(torch)}))
+        return
     log("config 3 layer, batch 1")
     lay = moe_layer_bench(torch, capi, 1, args.steps, args.warmup)
     log("  %.2f us a step, %.1f GB/s" % (lay["ms_per_step"] * 1e3, lay["gbs"]))
@@ -506,7 +570,7 @@ def main():
         extra = {}
         only = set(args.only.split(","))
         for n_tok in (4, 32) if "3" in only else ():
-            lb = moe_layer_bench(torch, capi, n_tok, max(args.steps // 4, 64), 64)
+            lb = moe_layer_bench(torch, capi, n_tok, max(args.steps // 4, 64), 16)
             extra["qwen_moe_layer_iq3xxs_bs%d" % n_tok] = {"GB/s": round(lb["gbs"], 2),
                                                            "us_per_step": round(lb["ms_per_step"] * 1e3, 3)}
             del lb

@@ -41,6 +41,21 @@ def compile_one(src):
     return obj
 
 
+CALIB_SRC = os.path.join(HERE, "calib", "ceilings.hip")
+CALIB_LIB = os.path.join(HERE, "libosmos_calib.so")
+
+
+def build_calib():
+    """the roofline calibration kernels (bench.py --ceilings), a library of their own: not part of the product"""
+    tmp = CALIB_LIB + ".tmp"
+    cmd = [HIPCC] + [f for f in FLAGS if not f.startswith("-I")] + ["-shared", CALIB_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError("hipcc failed on calib/ceilings.hip:\n" + r.stderr)
+    os.replace(tmp, CALIB_LIB)
+    return CALIB_LIB
+
+
 def build(jobs=None):
     os.makedirs(OUT, exist_ok=True)
     srcs = sources()
@@ -52,6 +67,7 @@ def build(jobs=None):
     if r.returncode:
         raise RuntimeError("link failed:\n" + r.stderr)
     os.replace(tmp, LIB)
+    build_calib()
     return LIB
 
 
