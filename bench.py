@@ -249,7 +249,24 @@ def prefill_extras(torch, capi):
     tops = 2.0 * rows * cols * pairs_n / us / 1e6
     out["prefill_q4k_down_mmq_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
                                         "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
-    del W, wt, x8, dx, sx, y
+    # the dense sub-shape: one Q4_K expert 2048 -> 7168 over all 512 tokens (32 full tiles: no padded slots) - the
+    # compute-bound case of the same kernel
+    idx1 = torch.arange(n_tok, dtype=torch.int32, device="cuda")
+    x8d = torch.zeros(n_tok * cols, dtype=torch.int8, device="cuda")
+    dxd = torch.zeros(n_tok * cols // 32, device="cuda")
+    sxd = torch.zeros(n_tok * cols // 32, device="cuda")
+    assert L.mmq_x8_rows(capi.addr(x), cols, capi.addr(idx1), n_tok, cols, capi.addr(x8d), capi.addr(dxd),
+                         capi.addr(sxd), None)
+    one = torch.tensor([n_tok], dtype=torch.int32, device="cuda")
+    z = torch.zeros(1, dtype=torch.int32, device="cuda")
+    yd = torch.zeros(n_tok * rows, device="cuda")
+    us = graph_us(torch, lambda i, st: L.mmq_group(12, capi.addr(wt), capi.addr(one), 1, n_tok, rows, cols,
+                                                   capi.addr(x8d), capi.addr(dxd), capi.addr(sxd), capi.addr(z),
+                                                   capi.addr(yd), capi.addr(z), rows, st), 8)
+    tops = 2.0 * rows * cols * n_tok / us / 1e6
+    out["dense_q4k_down_mmq_int8_512tok"] = {"us": round(us, 2), "TOPS": round(tops, 2),
+                                             "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
+    del W, wt, x8, dx, sx, y, x8d, dxd, sxd, yd
     torch.cuda.empty_cache()
     # IQ2_XXS gate on f16 MFMA: rows 2048, cols 7168
     rows, cols = 2048, 7168

@@ -25,7 +25,6 @@ namespace lgemm {
 
 using namespace lane;
 
-constexpr int kWaves = 4, kThreads = kWave * kWaves;
 constexpr uint32_t kTile = 16;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -157,9 +156,11 @@ __device__ inline void scales<kIQ1_M>(lbytes b, int j, float& d, int& s0, int& s
   d = f16((a0 >> 12) | ((a1 >> 8) & 0x00F0) | ((a2 >> 4) & 0x0F00) | (a3 & 0xF000));
 }
 
-// token tiles a pass at 16 / 32 logical lanes (the waves' chains: 64 / 32 VGPRs; at 32 lanes a second tile's 32 more
-// cost more occupancy than its shared decode saves)
-constexpr int kCT16 = 4, kCT32 = 1;
+// token tiles a pass and waves a workgroup at 16 / 32 logical lanes: the waves split the logical lanes, so a wave holds
+// L / W chains x CT tiles x 4 accumulators (64 / 32 VGPRs), and each decoded block serves CT tiles. measured on config
+// 5's IQ2_XXS gate (32 lanes): 4 waves and one tile 1.98 ms; 8 waves (so four tiles fit) 3.2 ms, 8 waves and two
+// tiles 2.2 ms - most of its experts hold one tile, and the larger workgroups halve the occupancy
+constexpr int kCT16 = 4, kCT32 = 1, kW16 = 4, kW32 = 4;
 
 template <uint32_t T>
 constexpr uint32_t grid_bytes_of() {
@@ -168,7 +169,7 @@ constexpr uint32_t grid_bytes_of() {
 
 // dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the sign masks, the waves' scale tables
 // and their partial trees
-template <uint32_t T, int CT>
+template <uint32_t T, int CT, int W>
 struct Lds {
   uint32_t slab, grid, sm, part, total;
   __host__ __device__ Lds(uint32_t rb) {
@@ -176,19 +177,20 @@ struct Lds {
     grid = (16 * rb + 15) / 16 * 16;
     sm = grid + grid_bytes_of<T>();
     part = sm + 128 * 8;
-    total = part + kWaves * CT * 4 * kWave * 4;
+    total = part + W * CT * 4 * kWave * 4;
   }
 };
 
 // blockIdx.x: 16 rows; blockIdx.y: the matrix, its cnt[m] tokens from row xrow[m] of q / d, CT tiles of 16 a pass.
-// wave w takes the blocks s = w (mod 4): its chains are the logical lanes ll = w (mod 4), L / 4 accumulators an
-// output; the xor tree's levels L/2 .. 4 pair chains of one wave (in registers), its levels 2 and 1 pair the waves
+// wave w takes the blocks s = w (mod W): its chains are the logical lanes ll = w (mod W), L / W accumulators an
+// output; the xor tree's levels L/2 .. W pair chains of one wave (in registers), its levels W/2 .. 1 pair the waves
 // (through LDS) - the same additions as the tree
-template <uint32_t T, int L, int CT>
-__global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
+template <uint32_t T, int L, int CT, int W>
+__global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
                                                    const int32_t* __restrict__ xrow, uint32_t cols,
                                                    const int8_t* __restrict__ q, const float* __restrict__ d,
                                                    float* __restrict__ y, uint32_t ys) {
+  constexpr int kWaves = W, kThreads = W * kWave;
   constexpr int per = (int) (Block<T>::values / 32), C = L / kWaves;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
@@ -196,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, col = lane % 16, quad = lane / 16;
   const uint32_t row0 = blockIdx.x * kTile, nblk = cols / 32, r0 = (uint32_t) xrow[m];
   const uint32_t rb = (uint32_t) row_bytes<T>(cols);
-  const Lds<T, CT> L_(rb);
+  const Lds<T, CT, W> L_(rb);
   // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
   {
     const u32x4* src = (const u32x4*) (w[m] + (uint64_t) row0 * rb);
@@ -296,33 +298,39 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* const* __restr
 #pragma unroll
       for (int i = 0; i < 4; i++) part[((wave * CT + ct) * 4 + i) * kWave + lane] = acc[0][ct][i];
     __syncthreads();
-    if (wave == 0) {  // levels 2 and 1: (T0 + T2) + (T1 + T3), T_w the wave's subtree (logical lanes w mod 4)
+    // levels W/2 .. 1 across the waves (T_w: wave w's subtree, logical lanes w mod W): each pass pairs w with
+    // w + o for w < o, as the tree pairs logical lanes ll and ll ^ o. the CT 4 outputs of a lane are shared out
+    // over the waves: wave v finishes outputs v, v + W, ...
+    {
+      const uint32_t wv = CT * 4 * kWave;  // a wave's stride
+      for (int oi = (int) wave; oi < CT * 4; oi += kWaves) {
+        const int ct = oi / 4, i = oi % 4;
+        const float* pp = part + (ct * 4 + i) * kWave + lane;
+        float t[kWaves];
 #pragma unroll
-      for (int ct = 0; ct < CT; ct++) {
+        for (int v = 0; v < kWaves; v++) t[v] = pp[v * wv];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const uint32_t t = c0 + ct * kTile + 4 * quad + i;  // (D: token 4 quad + i, row col)
-          const float* pp = part + (ct * 4 + i) * kWave + lane;
-          const uint32_t wv = CT * 4 * kWave;  // a wave's stride
-          const float v = __fadd_rn(__fadd_rn(pp[0], pp[2 * wv]), __fadd_rn(pp[wv], pp[3 * wv]));
-          if (t < n) y[(uint64_t) (r0 + t) * ys + row0 + col] = v;
-        }
+        for (int o = kWaves / 2; o > 0; o >>= 1)
+#pragma unroll
+          for (int v = 0; v < o; v++) t[v] = __fadd_rn(t[v], t[v + o]);
+        const uint32_t tk = c0 + ct * kTile + 4 * quad + i;  // (D: token 4 quad + i, row col)
+        if (tk < n) y[(uint64_t) (r0 + tk) * ys + row0 + col] = t[0];
       }
     }
     __syncthreads();  // the partial trees read before the next pass writes them
   }
 }
 
-template <uint32_t T, int L, int CT>
+template <uint32_t T, int L, int CT, int W>
 bool launch(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t rows,
             uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
-  const Lds<T, CT> l((uint32_t) row_bytes<T>(cols));
+  const Lds<T, CT, W> l((uint32_t) row_bytes<T>(cols));
   if (l.total > 160 * 1024) return false;
-  auto k = kernel<T, L, CT>;
+  auto k = kernel<T, L, CT, W>;
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
-  k<<<dim3(rows / kTile, n_mat), kThreads, l.total, s>>>((const uint8_t* const*) w, cnt, xrow, cols, q, d, y, ys);
+  k<<<dim3(rows / kTile, n_mat), W * kWave, l.total, s>>>((const uint8_t* const*) w, cnt, xrow, cols, q, d, y, ys);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -331,8 +339,8 @@ bool by_lanes(const void* const* w, const int32_t* cnt, const int32_t* xrow, uin
               uint32_t rows, uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
   if (cols % Block<T>::values) return false;
   (void) max_cnt;
-  return cols >= 4096 ? launch<T, 32, kCT32>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s)
-                      : launch<T, 16, kCT16>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s);
+  return cols >= 4096 ? launch<T, 32, kCT32, kW32>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s)
+                      : launch<T, 16, kCT16, kW16>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s);
 }
 
 }  // namespace lgemm

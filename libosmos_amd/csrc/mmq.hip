@@ -126,14 +126,14 @@ __global__ __launch_bounds__(kThreads) void q4k_kernel(const uint8_t* const* __r
   __shared__ __attribute__((aligned(16))) float xds[2][CT * kDxTile];  // [0] dx, [1] sx
   __shared__ float scl[kWaves][kGroups][2][kTile];  // a block's 16 rows' (d sc, dmin m) by group, a wave's own
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
-  if (!n) return;  // (the whole workgroup)
+  if (n <= blockIdx.z * kTile * CT) return;  // (the whole workgroup: no pass of its own)
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, col = lane % kTile, quad = lane / kTile;
   const uint32_t row0 = blockIdx.x * kTile * kWaves + wave * kTile;
   const bool live_rows = row0 < rows;  // (a wave past the rows still stages and meets the barriers)
   const uint32_t nb = cols / 256, rb = nb * kBlockBytes, groups = cols / MMQ_GROUP;
   const uint8_t* arow = wt[m] + (uint64_t) (live_rows ? row0 + col : 0) * rb;  // this lane's A row
   float* y = ya + yoff[m];
-  for (uint32_t c0 = 0; c0 < n; c0 += kTile * CT) {
+  for (uint32_t c0 = blockIdx.z * kTile * CT; c0 < n; c0 += gridDim.z * kTile * CT) {  // (passes over blockIdx.z)
     const uint32_t s0 = soff[m] + c0;  // the pass's first slot: a multiple of 16
     const int live = (int) ((n - c0 + kTile - 1) / kTile), tiles = live < CT ? live : CT;
     // a block's activations for the live tiles, into registers
@@ -247,13 +247,17 @@ __global__ __launch_bounds__(kThreads) void q4k_kernel(const uint8_t* const* __r
   }
 }
 
+// the token passes of a matrix spread over blockIdx.z: enough workgroups for the chip when few matrices hold many
+// tokens (one expert at 512 tokens: 112 row blocks x 8), each workgroup a pass in every Z
 template <int CT>
-bool q4k_launch(const void* const* w, const int32_t* cnt, uint32_t n_mat, uint32_t rows, uint32_t cols,
-                const int8_t* x8, const float* dx, const float* sx, const uint32_t* soff, float* y,
+bool q4k_launch(const void* const* w, const int32_t* cnt, uint32_t n_mat, uint32_t max_cnt, uint32_t rows,
+                uint32_t cols, const int8_t* x8, const float* dx, const float* sx, const uint32_t* soff, float* y,
                 const uint32_t* yoff, uint32_t ys, hipStream_t s) {
-  const uint32_t per = kTile * kWaves;
-  q4k_kernel<CT><<<dim3((rows + per - 1) / per, n_mat), kThreads, 0, s>>>((const uint8_t* const*) w, cnt, rows, cols,
-                                                                           x8, dx, sx, soff, y, yoff, ys);
+  const uint32_t per = kTile * kWaves, bx = (rows + per - 1) / per, passes = (max_cnt + kTile * CT - 1) / (kTile * CT);
+  uint32_t z = 1;
+  while (z < passes && (uint64_t) bx * n_mat * z < 2048) z *= 2;  // (about 8 workgroups a CU at most)
+  q4k_kernel<CT><<<dim3(bx, n_mat, min(z, passes)), kThreads, 0, s>>>((const uint8_t* const*) w, cnt, rows, cols,
+                                                                        x8, dx, sx, soff, y, yoff, ys);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -286,7 +290,9 @@ extern "C" OSM_API bool mmq_group(uint32_t type, const void* const* w, const int
       rows % mmq::kTile || !cols || cols % 256 || ys < rows)
     return false;
   const hipStream_t s = (hipStream_t) stream;
-  // (at most 2 tiles a pass: 4 hold 186 VGPRs, occupancy 2, and run the batch-512 down 1.45x slower)
-  if (max_cnt <= mmq::kTile) return mmq::q4k_launch<1>(w, cnt, n_mat, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
-  return mmq::q4k_launch<2>(w, cnt, n_mat, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
+  // (at most 2 tiles a pass: 4 hold 186 VGPRs, occupancy 2, and run the batch-512 down 1.45x slower, the dense
+  // 512-token expert 1.3x slower)
+  if (max_cnt <= mmq::kTile)
+    return mmq::q4k_launch<1>(w, cnt, n_mat, max_cnt, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
+  return mmq::q4k_launch<2>(w, cnt, n_mat, max_cnt, rows, cols, x8, dx, sx, soff, y, yoff, ys, s);
 }

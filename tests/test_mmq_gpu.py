@@ -84,3 +84,31 @@ def test_refusals(g):
     assert not L.mmq_group(12, p, p, 1, 1, 20, 256, p, p, p, p, p, p, 20, None)
     assert not L.mmq_group(12, p, p, 1, 1, 16, 250, p, p, p, p, p, p, 16, None)
     assert not L.mmq_x8_rows(p, 16, p, 1, 48, p, p, p, None)
+
+
+def test_group_dense_passes_split(g):
+    """one matrix over 200 tokens (7 passes of two tiles, spread over workgroups along z): the oracle's bits on a row
+    subset, and each of three tokens alone the same bits as in the batch"""
+    import torch
+    rows, cols, n = 128, 2048, 200
+    t = synth.ID["Q4_K"]
+    w = synth.random_blocks(t, rows, cols, 91)
+    x = np.random.default_rng(92).normal(0, 1, (n, cols)).astype(np.float32)
+    idx = np.arange(n, dtype=np.int32)
+    x8, dx, sx = x8_dev(g, x, idx, cols)
+    o8, odx, osx = orc.mmq_x8_rows(x, idx, cols)
+    z = np.zeros(1, np.uint32)
+    y = torch.full((n * rows,), float("nan"), device="cuda")
+    print("mmq_group dense 200", flush=True)
+    g.call("mmq_group", t, g.a(g.table([g.dev(w)])), g.a(g.dev(np.array([n], np.int32))), 1, n, rows, cols, g.a(x8),
+           g.a(dx), g.a(sx), g.a(g.dev(z)), g.a(y), g.a(g.dev(z)), rows, None)
+    yh = g.host(y).reshape(n, rows)
+    for k in range(0, n, 7):
+        want = orc.mmq_rows(w, rows, cols, o8, odx, osx, k)
+        assert (g.bits(yh[k]) == g.bits(want)).all(), k
+    for k in (0, 101, 199):
+        a8, adx, asx = x8_dev(g, x, [k], cols)
+        y1 = torch.full((rows,), float("nan"), device="cuda")
+        g.call("mmq_group", t, g.a(g.table([g.dev(w)])), g.a(g.dev(np.array([1], np.int32))), 1, 1, rows, cols,
+               g.a(a8), g.a(adx), g.a(asx), g.a(g.dev(z)), g.a(y1), g.a(g.dev(z)), rows, None)
+        assert (g.bits(g.host(y1)) == g.bits(yh[k])).all(), k
