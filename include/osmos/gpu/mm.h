@@ -2,9 +2,11 @@
    the entry points the prefill and expert batches bind: mm_known, mm_fits, mm_col_tiles, mm_x16, mm_x16_rows, mm_run,
    mm_group). contract (reference include/osmos/gpu/mm.h:119-200): each weight's exact value (decode.h, the mv
    contract's values) rounded to f16, times the f16 activations (x16, tiled as mm_x16 lays them), accumulated in F32
-   on gfx950's MFMA (v_mfma_f32_16x16x32_f16), K in ascending 32-value steps - a token's sums its own, so the same bits
-   at any batch and any tiling; within (cols/16 + 20) u sum |w16 x16| of the double sum over the values it reads (the
-   reference's own bound, tests/gpu/test_mm_gpu.hip:321-341). types: Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K,
+   on gfx950's MFMA (v_mfma_f32_16x16x32_f16) in the reference's K split (kernels/mm.hip:24-73): per type and width
+   SL-value slabs over W partitions, partition p the slabs p, p + W, ... as one chain of 32-value steps from zero, the
+   partitions' sums then added in order - a token's sums its own, so the same bits at any batch and any tiling;
+   within (cols/16 + 20) u sum |w16 x16| of the double sum over the values it reads (the reference's own bound,
+   tests/gpu/test_mm_gpu.hip:321-341). types: Q8_0, Q4_0, IQ4_NL, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K,
    IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ1_S, IQ1_M, IQ4_XS (GGUF ids). queued on `stream`, never waited for; false =
    refused, nothing queued. */
 #ifndef MM_H
@@ -23,10 +25,10 @@ extern "C" {
 
 /* replaces reference include/osmos/gpu/mm.h:11 (kernels/mm.hip): whether `type` has an mm kernel here */
 bool mm_known(uint32_t type);
-/* replaces reference include/osmos/gpu/mm.h:12: rows whole tiles (16), cols whole blocks of the type and whole
-   32-value steps */
+/* replaces reference include/osmos/gpu/mm.h:12: rows whole tiles (16), cols whole blocks of the type and whole slabs
+   of the type's shape for that width (under 2048 columns Q6_K's 64; a width Q8_0's 128 does not divide: 64) */
 bool mm_fits(uint32_t type, uint32_t rows, uint32_t cols);
-/* replaces reference include/osmos/gpu/mm.h:13: the token tiles (of 16) a decoded weight step feeds at n tokens, 1 .. 4;
+/* replaces reference include/osmos/gpu/mm.h:13: the token tiles (of 16) a decoded weight step feeds at n tokens, 1 .. 8;
    0 for a type without a kernel */
 uint32_t mm_col_tiles(uint32_t type, uint32_t n);
 /* replaces reference include/osmos/gpu/mm.h:14: n rows of cols F32 (row t at x + t xs) to f16 (nearest) in x16's
@@ -45,8 +47,9 @@ bool mm_x16_rows(const float *x, uint32_t xs, const int32_t *idx, uint32_t slots
                  int32_t *overflow, void *stream);
 /* replaces reference include/osmos/gpu/mm.h:38-40: n_mat matrices of one type and shape: matrix m (w[m]) over the
    tiled x16 from x16 + xoff[m] halves (rows xts long, its first token at a tile start), its first cnt[m] tokens
-   (at most max_cnt <= MM_MAX_TOKENS) into y + yoff[m] + t ys - each tile the sums mm_run gives. w, cnt, xoff, yoff on
-   the device */
+   (at most max_cnt <= MM_MAX_TOKENS) into y + yoff[m] + t ys - each tile the sums mm_run gives (the type's tuned
+   shape at every width: Q6_K under 2048 columns splits K otherwise than mm_run, as the reference's does). cols whole
+   128-value slabs. w, cnt, xoff, yoff on the device */
 bool mm_group(uint32_t type, const void *const *w, const int32_t *cnt, uint32_t n_mat, uint32_t max_cnt, uint32_t rows,
               uint32_t cols, const void *x16, const uint32_t *xoff, uint32_t xts, float *y, const uint32_t *yoff,
               uint32_t ys, void *stream);

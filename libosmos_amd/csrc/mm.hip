@@ -1,15 +1,15 @@
 // libosmos MI355X - the quantized weights' f16 matrix products (include/osmos/gpu/mm.h): mm_known, mm_fits,
 // mm_col_tiles, mm_x16, mm_x16_rows, mm_run, mm_group.
 //
-// contract (reference include/osmos/gpu/mm.h:119-200, kernels/mm.h): y = W x over each weight's exact value rounded
-// to f16 (RNE) and the f16 activations, products exact in F32 and summed in F32 by the matrix cores.
+// contract (reference include/osmos/gpu/mm.h:87-200, kernels/mm.hip:24-73, kernels/mm.h:84-90): y = W x over each
+// weight's exact value rounded to f16 (RNE) and the f16 activations, products exact in F32; K split the reference's
+// way for the type and width - W partitions, partition p the slabs p, p + W, ... (SL values each), one chain of
+// matrix-core steps from zero each, then the partitions summed in order. a token's sums its own: the same bits at any
+// batch, tiling or grouping.
 //
-// CDNA4 mapping: a wave owns 16 rows; each 32-value K step it decodes its A operand straight into registers - lane l
-// the 8 values 8 (l / 16) .. + 7 of row l % 16 (decode.h's chunk, the mv contract's exact values), then f16 - and runs
-// v_mfma_f32_16x16x32_f16 against up to CT token tiles of x16 (lane l's B operand the same 8 columns of token l % 16:
-// one 16-byte load from the tiled layout). A and B fill the same lane slots with the same columns, so the product is
-// the dot product whatever order the unit takes K in; the accumulator of a token depends on that token's column
-// alone, the K steps always in ascending order - the same bits at any batch size, tile count or grouping.
+// CDNA4 mapping: a workgroup is 16 rows x W waves, wave p partition p; each step is v_mfma_f32_16x16x32_f16 (32
+// values: the gfx950 f16 MMA's K, the reference's WMMA takes 16) - A the lane's row's 8 decoded values, B the same 8
+// columns of its token.
 #include <type_traits>
 
 #include "decode.h"
@@ -27,8 +27,7 @@ __constant__ DecodeTables kDec = make_decode_tables();
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4, kThreads = kWave * kWaves;
-constexpr uint32_t kTile = kX16Tile, kRowsWave = 16, kRowsWg = kRowsWave * kWaves, kStep = 32;
+constexpr uint32_t kTile = kX16Tile, kStep = 32;
 
 struct Args {
   const uint8_t* w0;            // mm_run's matrix (wt NULL)
@@ -63,26 +62,56 @@ __device__ inline void fill_tab(LdsTab<T>& t) {  // every thread of the workgrou
   else if constexpr (T == kIQ3_XXS) src = (const uint32_t*) kDec.g.iq3xxs, words = sizeof t / 4;
   else if constexpr (T == kIQ1_S || T == kIQ1_M) src = (const uint32_t*) kDec.g.iq1s, words = sizeof t / 4;
   else if constexpr (T == kIQ4_NL || T == kIQ4_XS) src = (const uint32_t*) kDec.iq4nl, words = 4, dst = (uint32_t*) t.iq4nl;
-  for (uint32_t i = threadIdx.x; i < words; i += kThreads) dst[i] = src[i];
+  for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
 }
 
-// values a staged chunk of a row: whole blocks, about 256 bytes of a row (16 KB for the workgroup's 64 rows)
-template <uint32_t T>
-constexpr uint32_t chunk_values() {
-  constexpr uint32_t v = Block<T>::values, b = Block<T>::bytes, per256 = 256 / v * b;
-  return v == 1 ? 64 : per256 <= 72 ? 1024 : per256 <= 144 ? 512 : 256;
+// a type's K split (reference kernels/mm.hip:24-73, the Tuned / Short / Odd shapes): SL values a slab, W partitions.
+// partition p takes the slabs p, p + W, ... of a row; each partition one chain of MMAs from zero in K order; then the
+// partitions' sums added in order, s = part 0, s += part 1, ... a matrix's shape is its type's and its width's, never
+// its tokens': a token's bits are the same at any batch
+struct KSplit {
+  uint32_t sl, w;
+};
+template <uint32_t T> constexpr KSplit tuned() {
+  switch (T) {
+    case kQ5_K: return {32, 8};
+    case kQ4_K: return {32, 16};
+    case kIQ1_M: case kIQ1_S: case kIQ2_XXS: case kIQ2_XS: case kIQ2_S: return {128, 4};
+    case kIQ4_NL: case kIQ4_XS: case kQ4_0: return {64, 4};
+    case kQ2_K: case kQ3_K: return {64, 8};
+    default: return {128, 8};  // Q8_0, Q6_K, IQ3_XXS
+  }
+}
+constexpr uint32_t kShortCols = 2048;  // under it mm_run takes the type's short shape (Q6_K: 64 x 8)
+template <uint32_t T> constexpr KSplit short_shape() { return T == kQ6_K ? KSplit{64, 8} : tuned<T>(); }
+// a width the slab does not divide: Q8_0's 64 x 2 (others: none - mm_fits refuses)
+template <uint32_t T> constexpr KSplit odd_shape() { return T == kQ8_0 ? KSplit{64, 2} : short_shape<T>(); }
+// mm_run's shape for a width (group: mm_group's - the tuned shape whatever the width)
+template <uint32_t T> KSplit shape_of(uint32_t cols, bool group) {
+  if (group) return tuned<T>();
+  const KSplit s = cols < kShortCols ? short_shape<T>() : tuned<T>();
+  return cols % s.sl ? odd_shape<T>() : s;
 }
 
-// blockIdx.x: 64 rows (a wave 16); blockIdx.y: the matrix; blockIdx.z: CT token tiles. the rows' bytes go through LDS a
-// chunk at a time (double-buffered: the next chunk's loads in flight while this one is decoded), W bytes a load (4
-// where every row's chunk is 4-aligned, else 2); the type's codebook is copied into LDS once. each wave decodes its 16
-// rows from LDS and runs the K steps in ascending order, as the unstaged kernel did: the same sums, the same bits
-template <uint32_t T, int CT, int W>
-__global__ __launch_bounds__(kThreads) void kernel(Args a) {
-  typedef typename std::conditional<W == 4, uint32_t, uint16_t>::type word;
-  constexpr uint32_t kCv = chunk_values<T>(), kCb = kCv / Block<T>::values * Block<T>::bytes;  // a row's chunk
-  constexpr uint32_t kWords = kRowsWg * kCb / W, kPer = (kWords + kThreads - 1) / kThreads;
-  __shared__ __attribute__((aligned(16))) uint8_t wbuf[2][kRowsWg * kCb];
+// blockIdx.x: RT tiles of 16 rows; blockIdx.y: the matrix; blockIdx.z: CT token tiles. W waves, wave p the partition
+// p. the rows go through LDS a round at a time (a round: W slabs, whole blocks - every partition's next slab),
+// double-buffered: the next round's loads in flight while this one is decoded; the type's codebook in LDS once. in a
+// round wave p decodes its slab of each row tile (lane l: row l % 16, the 8 values 8 (l / 16) .. of each 32-value
+// step, decode.h's exact values rounded to f16) into its A operands and runs v_mfma_f32_16x16x32_f16 against each
+// token tile (B: the same 8 columns of token l % 16, one 16-byte load of the tiled x16) - A and B fill the same lane
+// slots with the same columns, so each step is its 32 values' dot product whatever order the unit takes them in.
+// then the partitions' tiles are summed in order through LDS. RT and CT are the tiling alone: the same sums
+template <uint32_t T, uint32_t SL, int W, int CT, int RT, int WB>
+__global__ __launch_bounds__(W * kWave) void kernel(Args a) {
+  typedef typename std::conditional<WB == 4, uint32_t, uint16_t>::type word;
+  constexpr int kThreads = W * kWave;
+  constexpr uint32_t kRows = kTile * RT;                                // the workgroup's rows
+  constexpr uint32_t kRv = SL * W;                                      // a round's values a row
+  constexpr uint32_t kRb = kRv / Block<T>::values * Block<T>::bytes;    // its bytes
+  static_assert(kRv % Block<T>::values == 0, "a round whole blocks");
+  constexpr uint32_t kWords = kRows * kRb / WB, kPer = (kWords + kThreads - 1) / kThreads, kWr = kRb / WB;
+  constexpr uint32_t kStage = 2 * kRows * kRb, kPart = W * 4 * kWave * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kStage > kPart ? kStage : kPart];
   __shared__ LdsTab<T> tab;
   const uint32_t m = blockIdx.y;
   const uint8_t* w = a.w0;
@@ -93,82 +122,98 @@ __global__ __launch_bounds__(kThreads) void kernel(Args a) {
     w = a.wt[m], n = (uint32_t) a.cnt[m];
     x16 += a.xoff[m], y += a.yoff[m];
   }
-  const uint32_t t0 = blockIdx.z * kTile * CT, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const uint32_t rbase = blockIdx.x * kRowsWg, row0 = rbase + wave * kRowsWave;
+  const uint32_t t0 = blockIdx.z * kTile * CT, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, q = lane / 16;
+  const uint32_t row0 = blockIdx.x * kRows;
   if (t0 >= n) return;  // (uniform: the whole workgroup)
-  const bool live = row0 < a.rows;  // (a wave past the rows stages and meets the barriers, computes nothing)
-  const uint32_t rb = (uint32_t) row_bytes<T>(a.cols), q = lane / 16;
-  // this thread's staged words: word i of the chunk is row i / (kCb / W), word i % (kCb / W) of it; its source a 32-bit
-  // byte offset from the matrix (one expert's matrix is far under 4 GB) plus the chunk's
-  constexpr uint32_t kWr = kCb / W;  // words a row's chunk
+  const int tiles = (int) ((n - t0 + kTile - 1) / kTile) < CT ? (int) ((n - t0 + kTile - 1) / kTile) : CT;
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.cols);
+  // this thread's staged words: word i of a round is row i / kWr's word i % kWr, at a 32-bit offset from the matrix
+  // (rows past the matrix: its last, staged and not stored)
   uint32_t woff[kPer];
 #pragma unroll
-  for (int u = 0; u < kPer; u++) {
-    const uint32_t i = min((uint32_t) (u * kThreads) + threadIdx.x, kWords - 1);
-    const uint32_t gr = min(rbase + i / kWr, a.rows - 1);  // (rows past the matrix: its last, staged and not used)
-    woff[u] = gr * rb + (i % kWr) * W;
+  for (uint32_t u = 0; u < kPer; u++) {
+    const uint32_t i = min(u * kThreads + threadIdx.x, kWords - 1);
+    woff[u] = min(row0 + i / kWr, a.rows - 1) * rb + (i % kWr) * WB;
   }
   word wr[kPer];
-  const uint32_t nch = (a.cols + kCv - 1) / kCv;
-  auto load = [&](uint32_t c) __attribute__((always_inline)) {
-    // (a short last chunk: the words past its end read its last word instead - loaded, never decoded)
-    const uint32_t lim = (a.cols - c * kCv) / Block<T>::values * Block<T>::bytes;  // the chunk's bytes a row
-    const uint8_t* base = w + (uint64_t) c * kCb;
+  const uint32_t nr = (a.cols + kRv - 1) / kRv;  // rounds (the last may be short: its missing slabs skipped)
+  auto load = [&](uint32_t r) __attribute__((always_inline)) {
+    const uint32_t lim = (a.cols - r * kRv) / Block<T>::values * Block<T>::bytes;  // the round's bytes a row
+    const uint8_t* base = w + (uint64_t) r * kRb;
 #pragma unroll
-    for (int u = 0; u < kPer; u++) {
-      const uint32_t o = (u * kThreads + threadIdx.x) % kWr * W;
-      wr[u] = *(const word*) (base + woff[u] - (o < lim ? 0 : o - (lim - W)));
+    for (uint32_t u = 0; u < kPer; u++) {
+      const uint32_t o = (u * kThreads + threadIdx.x) % kWr * WB;
+      wr[u] = *(const word*) (base + woff[u] - (o < lim ? 0 : o - (lim - WB)));  // (past a short round: its last word)
     }
   };
   auto store = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < kPer; u++)
-      if (u * kThreads + threadIdx.x < kWords) ((word*) wbuf[buf])[u * kThreads + threadIdx.x] = wr[u];
+    for (uint32_t u = 0; u < kPer; u++)
+      if (u * kThreads + threadIdx.x < kWords) ((word*) (smem + buf * kRows * kRb))[u * kThreads + threadIdx.x] = wr[u];
   };
   fill_tab<T>(tab);
   load(0);
   store(0);
-  if (nch > 1) load(1);
+  if (nr > 1) load(1);
   __syncthreads();
   const _Float16* xb = x16 + x16_at(t0 + lane % 16, 8 * q, a.xts);
-  f32x4 acc[CT];
+  f32x4 acc[RT][CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ct++) acc[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (uint32_t c = 0; c < nch; c++) {
-    const int buf = (int) (c % 2);
-    if (c + 1 < nch) store(buf ^ 1);  // (buffer buf ^ 1's last reads were before the previous barrier)
-    if (c + 2 < nch) load(c + 2);
-    const uint32_t k_end = min(kCv, a.cols - c * kCv);
-    const uint8_t* row = wbuf[buf] + (wave * kRowsWave + lane % 16) * kCb;
-    if (live) {
-      for (uint32_t k0 = 0; k0 < k_end; k0 += kStep) {
-        float v[kChunk];
-        int k;
-        const uint8_t* b = chunk_at<T>(row, k0 / kChunk + q, &k);
-        decode<T>(tab, b, k, v);
-        half8 av;
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int i = 0; i < kChunk; i++) av[i] = (_Float16) v[i];  // nearest, ties to even
-        const uint32_t kk = c * kCv + k0;
+    for (int ct = 0; ct < CT; ct++) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t r = 0; r < nr; r++) {
+    const int buf = (int) (r % 2);
+    if (r + 1 < nr) store(buf ^ 1);  // (buffer buf ^ 1's last reads were before the previous barrier)
+    if (r + 2 < nr) load(r + 2);
+    const uint32_t k_slab = r * kRv + wave * SL;  // this wave's slab of the round
+    if (k_slab < a.cols) {  // (uniform in the wave)
+#pragma unroll
+      for (uint32_t k0 = 0; k0 < SL; k0 += kStep) {
+        half8 av[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+          const uint8_t* row = smem + buf * kRows * kRb + (rt * kTile + lane % 16) * kRb;
+          float v[kChunk];
+          int k;
+          const uint8_t* b = chunk_at<T>(row, (wave * SL + k0) / kChunk + q, &k);
+          decode<T>(tab, b, k, v);
+#pragma unroll
+          for (int i = 0; i < kChunk; i++) av[rt][i] = (_Float16) v[i];  // nearest, ties to even
+        }
+        const uint32_t kk = k_slab + k0;
 #pragma unroll
         for (int ct = 0; ct < CT; ct++)
-          if (t0 + ct * kTile < n) {  // (uniform) the tiles that exist
+          if (ct < tiles) {  // (uniform) the tiles that exist
             const half8 bv = *(const half8*) (xb + (uint64_t) ct * kTile * a.xts + (kk / 16) * 256);
-            acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[ct], 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+              acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt], bv, acc[rt][ct], 0, 0, 0);
           }
       }
     }
-    __syncthreads();  // chunk c read by every wave; chunk c + 1 stored
+    __syncthreads();  // round r read by every wave; round r + 1 stored
   }
-  if (!live) return;
-  // the accumulator: lane l holds rows 4 (l / 16) + i of the wave's 16, token l % 16 of the tile
+  // the partitions' sums in order, a tile at a time through LDS (the staging buffers free now): lane l of wave p holds
+  // partition p's rows 4 (l / 16) + i, token l % 16 of the tile; register i's outputs are summed by wave i % W
+  float* part = (float*) smem;
 #pragma unroll
-  for (int ct = 0; ct < CT; ct++) {
-    const uint32_t t = t0 + ct * kTile + lane % 16;
-    if (t < n)
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) y[(uint64_t) t * a.ys + row0 + 4 * q + i] = acc[ct][i];
-  }
+    for (int ct = 0; ct < CT; ct++) {
+      if (ct >= tiles) break;  // (uniform)
+      if (rt || ct) __syncthreads();  // the tile before summed
+#pragma unroll
+      for (int i = 0; i < 4; i++) part[(wave * 4 + i) * kWave + lane] = acc[rt][ct][i];
+      __syncthreads();
+      const uint32_t t = t0 + ct * kTile + lane % 16, r = row0 + rt * kTile + 4 * q;
+      for (int i = (int) wave; i < 4; i += W) {
+        float sum = part[i * kWave + lane];
+#pragma unroll
+        for (int p = 1; p < W; p++) sum = __fadd_rn(sum, part[(p * 4 + i) * kWave + lane]);
+        if (t < n && r + i < a.rows) y[(uint64_t) t * a.ys + r + i] = sum;
+      }
+    }
 }
 
 // F32 rows to the tiled f16: a thread 8 columns of one token (16 bytes out); rows at or past n zero. Rows: token t is
@@ -211,39 +256,62 @@ __global__ __launch_bounds__(256) void x16_kernel(const float* __restrict__ x, u
   if (over && overflow) *overflow = 1;
 }
 
+// token tiles a decoded step feeds (the reference's most: 8): the accumulators are 4 VGPRs a tile
 constexpr uint32_t col_tiles(uint32_t n) {
   const uint32_t t = (n + kTile - 1) / kTile;
-  return t >= 4 ? 4 : t >= 2 ? 2 : 1;
+  return t >= 8 ? 8 : t >= 4 ? 4 : t >= 2 ? 2 : 1;
 }
 
-template <uint32_t T, int CT>
-bool launch(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
-  const dim3 grid((a.rows + kRowsWg - 1) / kRowsWg, n_mat, (max_n + kTile * CT - 1) / (kTile * CT));
-  // 4-byte staging loads where every row's chunk starts 4-aligned (the row bytes and the chunk bytes multiples of 4:
+template <uint32_t T, uint32_t SL, int W, int CT, int RT>
+bool launch_s(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
+  const dim3 grid((a.rows + kTile * RT - 1) / (kTile * RT), n_mat, (max_n + kTile * CT - 1) / (kTile * CT));
+  // 4-byte staging loads where every row's round starts 4-aligned (the row bytes and the round bytes multiples of 4:
   // the weights themselves come from hipMalloc, 256-aligned, or a caller's whole-block slice of them)
-  constexpr uint32_t cb = chunk_values<T>() / Block<T>::values * Block<T>::bytes;
-  const bool w4 = row_bytes<T>(a.cols) % 4 == 0 && cb % 4 == 0;
-  if (w4)
-    kernel<T, CT, 4><<<grid, kThreads, 0, s>>>(a);
+  constexpr uint32_t rbr = SL * W / Block<T>::values * Block<T>::bytes;
+  if (row_bytes<T>(a.cols) % 4 == 0 && rbr % 4 == 0)
+    kernel<T, SL, W, CT, RT, 4><<<grid, W * kWave, 0, s>>>(a);
   else
-    kernel<T, CT, 2><<<grid, kThreads, 0, s>>>(a);
+    kernel<T, SL, W, CT, RT, 2><<<grid, W * kWave, 0, s>>>(a);
   return hipGetLastError() == hipSuccess;
 }
 
-template <uint32_t T>
-bool fits(uint32_t rows, uint32_t cols) {  // (a matrix under 4 GB: the staging's 32-bit offsets)
-  return rows && cols && rows % kTile == 0 && cols % Block<T>::values == 0 && cols % kStep == 0 &&
-         (uint64_t) rows * row_bytes<T>(cols) <= 0xFFFFFFFFull;
+// the tiling: a workgroup's row tiles RT (4 where the launch has row blocks enough for the chip at 64 rows - many
+// matrices, or a tall one - else 1) and token tiles CT (at most 8 / RT: the accumulators 4 RT CT VGPRs)
+template <uint32_t T, uint32_t SL, int W>
+bool launch_ct(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
+  const bool tall = (uint64_t) n_mat * (a.rows / 64) >= 1024;
+  const uint32_t ct = col_tiles(max_n);
+  if (tall) {
+    if (ct == 1) return launch_s<T, SL, W, 1, 4>(a, n_mat, max_n, s);
+    return launch_s<T, SL, W, 2, 4>(a, n_mat, max_n, s);
+  }
+  switch (ct) {
+    case 1: return launch_s<T, SL, W, 1, 1>(a, n_mat, max_n, s);
+    case 2: return launch_s<T, SL, W, 2, 1>(a, n_mat, max_n, s);
+    case 4: return launch_s<T, SL, W, 4, 1>(a, n_mat, max_n, s);
+    default: return launch_s<T, SL, W, 8, 1>(a, n_mat, max_n, s);
+  }
 }
 
 template <uint32_t T>
+bool fits_shape(uint32_t rows, uint32_t cols, bool group) {  // (a matrix under 4 GB: the staging's 32-bit offsets)
+  if (!rows || !cols || rows % kTile || cols % Block<T>::values || (uint64_t) rows * row_bytes<T>(cols) > 0xFFFFFFFFull)
+    return false;
+  if (group && cols % 128) return false;  // (mm_group: whole 128-value slabs, the reference's rule)
+  return cols % shape_of<T>(cols, group).sl == 0;
+}
+template <uint32_t T>
+bool fits(uint32_t rows, uint32_t cols) { return fits_shape<T>(rows, cols, false); }
+
+template <uint32_t T>
 bool run_by(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
-  if (!fits<T>(a.rows, a.cols)) return false;
-  switch (col_tiles(max_n)) {
-    case 1: return launch<T, 1>(a, n_mat, max_n, s);
-    case 2: return launch<T, 2>(a, n_mat, max_n, s);
-    default: return launch<T, 4>(a, n_mat, max_n, s);
-  }
+  const bool group = a.wt != nullptr;
+  if (!fits_shape<T>(a.rows, a.cols, group)) return false;
+  const KSplit k = shape_of<T>(a.cols, group);
+  constexpr KSplit t = tuned<T>(), sh = short_shape<T>(), od = odd_shape<T>();
+  if (k.sl == t.sl && k.w == t.w) return launch_ct<T, t.sl, (int) t.w>(a, n_mat, max_n, s);
+  if (k.sl == sh.sl && k.w == sh.w) return launch_ct<T, sh.sl, (int) sh.w>(a, n_mat, max_n, s);
+  return launch_ct<T, od.sl, (int) od.w>(a, n_mat, max_n, s);
 }
 
 #define OSM_MM_TYPES(X) \

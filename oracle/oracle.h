@@ -8,6 +8,8 @@
    - mv (fp32 activations): kernels/mv.h:1-70, kernels/quant.h:60-348, src/cpu/expert.c:10-253,
      include/osmos/gpu/mv.h:31-62;
    - mmq (Q4_K on int8 matrix cores): include/osmos/gpu/mmq.h:37-55, kernels/mmq.hip:33-151;
+   - mm (the f16 matmul's K split and partition order): include/osmos/gpu/mm.h:87-200, kernels/mm.hip:24-73,
+     kernels/mm.h:84-90 (a step's rounding modeled: exact where no step drops a bit - see mm.c);
    - the lane's layer (round x, gate/up + swiglu, round h, down, token sums by ascending expert): src/cpu/lane.c:71-118,
      src/run/hip_lane.c:164-220, kernels/ops.hip:502-516;
    - MoE plumbing: kernels/q4x_moe.hip:38-200 (route, expert tables, weighted sum).
@@ -66,6 +68,13 @@ bool orc_mv_known(uint32_t type);
 bool orc_dequant(uint32_t type, const void *src, uint64_t values, float *dst);
 bool orc_mv_rows(uint32_t type, const void *w, uint32_t cols, uint32_t r0, uint32_t r1, const float *x, uint32_t xs,
                  uint32_t n, float *y, uint32_t ys);
+
+/* mm (the f16 matmul's order): rows r0 .. r1 of a matrix of `type` against n tokens of x (row t at x + t xs, each
+   value rounded to f16), the reference's K split for the type and width (group: mm_group's); y[t ys + r] */
+float orc_f16_round(float v);
+void orc_mm_shape(uint32_t type, uint32_t cols, bool group, uint32_t *sl, uint32_t *w); /* the K split: slab, parts */
+bool orc_mm_rows(uint32_t type, const void *w, uint32_t cols, uint32_t r0, uint32_t r1, const float *x, uint32_t xs,
+                 uint32_t n, bool group, float *y, uint32_t ys);
 
 /* mmq contract (Q4_K) */
 uint64_t orc_mmq_x8_at(uint32_t s, uint32_t c, uint32_t cols);

@@ -57,6 +57,9 @@ def orc():
         _sig(lib, "orc_mmq_rows", B, P, U32, U32, U32, P, P, P, U32, P)
         _sig(lib, "orc_mmq_x8_at", U64, U32, U32, U32)
         _sig(lib, "orc_mmq_dx_at", U64, U32, U32, U32)
+        _sig(lib, "orc_f16_round", F32, F32)
+        _sig(lib, "orc_mm_shape", None, U32, U32, B, _c.POINTER(U32), _c.POINTER(U32))
+        _sig(lib, "orc_mm_rows", B, U32, P, U32, U32, U32, P, U32, U32, B, P, U32)
         _sig(lib, "orc_lane_layer", B, U32, U32, U32, U32, F32, P, P, U32, P, P, P, P, P, U32, P)
         _sig(lib, "orc_gather_sum_add", None, P, P, P, U32, U32, U32, P)
         _sig(lib, "orc_route", None, P, U32, U32, U32, P, P)
@@ -151,3 +154,19 @@ def mmq_rows(w, rows, cols, x8, dx, sx, slot):
     assert orc().orc_mmq_rows(ptr(np.ascontiguousarray(w, dtype=np.uint8)), cols, 0, rows, ptr(x8), ptr(dx), ptr(sx),
                               slot, ptr(y))
     return y
+
+
+def mm_rows(type_, w, rows, cols, x, group=False):
+    """the f16 matmul's order (mm_run, or mm_group's shape): w bytes of [rows, cols], x [n, cols] -> y [n, rows]"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[0]
+    y = np.zeros((n, rows), np.float32)
+    assert orc().orc_mm_rows(type_, ptr(np.ascontiguousarray(w, dtype=np.uint8)), cols, 0, rows, ptr(x), cols, n,
+                             group, ptr(y), rows)
+    return y
+
+
+def mm_shape(type_, cols, group=False):
+    sl, w = U32(), U32()
+    orc().orc_mm_shape(type_, cols, group, _c.byref(sl), _c.byref(w))
+    return sl.value, w.value

@@ -91,7 +91,8 @@ def test_queries():
         t = synth.ID[name]
         assert L.mm_known(t)
         assert L.mm_fits(t, 64, 512) and not L.mm_fits(t, 60, 512) and not L.mm_fits(t, 64, 0)
-        assert L.mm_col_tiles(t, 1) == 1 and L.mm_col_tiles(t, 17) == 2 and L.mm_col_tiles(t, 512) == 4
+        assert L.mm_col_tiles(t, 1) == 1 and L.mm_col_tiles(t, 17) == 2 and L.mm_col_tiles(t, 64) == 4
+        assert L.mm_col_tiles(t, 512) == 8
     assert not L.mm_known(0) and L.mm_col_tiles(0, 16) == 0
     assert not L.mm_fits(synth.ID["Q4_K"], 64, 128)  # not whole 256-value blocks
 
@@ -198,3 +199,32 @@ def test_swiglu_rows(g):
     assert (got[zv] == 0).all()
     assert np.isnan(got[~livev]).all()  # the tile's rows past the slots untouched
     assert int(g.host(ov)[0]) == 0
+
+
+@pytest.mark.parametrize("name,cols,group", [("Q8_0", 2048, False), ("Q8_0", 320, False), ("Q4_K", 2048, False),
+                                             ("Q5_K", 512, False), ("Q6_K", 1536, False), ("Q6_K", 1536, True),
+                                             ("Q4_0", 512, False), ("IQ4_NL", 512, False), ("Q2_K", 1024, False),
+                                             ("Q3_K", 1024, False), ("IQ2_XXS", 1024, False), ("IQ2_XS", 1024, True),
+                                             ("IQ2_S", 1024, False), ("IQ1_S", 1024, False), ("IQ1_M", 1024, True),
+                                             ("IQ3_XXS", 2048, True), ("IQ4_XS", 512, False)])
+def test_mm_partition_order(g, name, cols, group):
+    """the reference's K split, bit for bit: on data where every matrix-core step is exact (tests/mmorder.py) mm_run
+    (or mm_group) gives the oracle's bits - the partitions' chains and their ordered sum - which differ from a single
+    chain's in K order"""
+    import torch
+    from tests import mmorder
+    t = synth.ID[name]
+    w, x, ordered, chain = mmorder.case(name, cols, group, 7)
+    want = orc.mm_rows(t, w, 16, cols, x, group)
+    x16, _ = mm_x16(g, x)
+    n = x.shape[0]
+    print("mm order", name, cols, group, flush=True)
+    if group:
+        y = torch.full((n, 16), float("nan"), device="cuda")
+        z = np.zeros(1, np.uint32)
+        g.call("mm_group", t, g.a(g.table([g.dev(w)])), g.a(g.dev(np.array([n], np.int32))), 1, n, 16, cols, g.a(x16),
+               g.a(g.dev(z)), cols, g.a(y), g.a(g.dev(z)), 16, None)
+        got = g.host(y)
+    else:
+        got = run(g, name, w, 16, cols, x16, n)
+    assert (g.bits(got) == g.bits(want)).all()

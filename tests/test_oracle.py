@@ -453,3 +453,38 @@ def test_moe_sum_float64():
         exact = sum(terms)
         mag = sum(np.abs(a) for a in terms)
         assert np.all(np.abs(out[t] - exact) <= (k + 4) * 2.0 ** -24 * mag + 1e-30), t
+
+
+# ---- the f16 matmul's K order (orc_mm_rows) ----
+
+MM_ORDER_CASES = [("Q8_0", 2048, False), ("Q8_0", 320, False), ("Q4_K", 2048, False), ("Q5_K", 512, False),
+                  ("Q6_K", 1536, False), ("Q6_K", 1536, True), ("Q6_K", 2048, False), ("Q4_0", 512, False),
+                  ("IQ4_NL", 512, False), ("Q2_K", 1024, False), ("Q3_K", 1024, False), ("IQ2_XXS", 1024, False),
+                  ("IQ2_XS", 1024, True), ("IQ1_S", 1024, False), ("IQ3_XXS", 2048, True), ("IQ4_XS", 512, False)]
+
+
+@pytest.mark.parametrize("name,cols,group", MM_ORDER_CASES)
+def test_mm_rows_partition_order(name, cols, group):
+    """orc_mm_rows follows the reference's K split for the type and width (kernels/mm.hip:24-73): partition 0's two
+    nearly cancelling products and partition 1's small one give the value worked out by hand from the contract's
+    order (partitions first, then their sum in order), not the single K chain's (tests/mmorder.py)"""
+    from tests import mmorder
+    w, x, ordered, chain = mmorder.case(name, cols, group, 7)
+    y = orc.mm_rows(synth.ID[name], w, 16, cols, x, group)
+    assert (bits(y) == bits(np.repeat(ordered[:, None], 16, axis=1))).all()
+    assert (ordered != chain).all()
+
+
+def test_mm_rows_bound():
+    """on random weights and activations orc_mm_rows is within the reference's bound, (cols/16 + 20) u sum |w x|, of
+    the double sum over the f16-rounded values (tests/gpu/test_mm_gpu.hip:321-341)"""
+    rng = np.random.default_rng(3)
+    for name, cols in (("Q4_K", 1024), ("IQ2_XXS", 2048), ("Q8_0", 320)):
+        t = synth.ID[name]
+        w = synth.random_blocks(t, 8, cols, 5)
+        x = rng.normal(0, 1, (5, cols)).astype(np.float32)
+        y = orc.mm_rows(t, w, 8, cols, x)
+        wf = orc.dequant(t, w, 8 * cols).reshape(8, cols).astype(np.float16).astype(np.float64)
+        xf = x.astype(np.float16).astype(np.float64)
+        err = np.abs(y - xf @ wf.T)
+        assert (err <= (cols / 16 + 20) * 2.0 ** -24 * (np.abs(xf) @ np.abs(wf).T)).all(), name
