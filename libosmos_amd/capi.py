@@ -116,6 +116,29 @@ SIGS.update({
     "gguf_int": (B, [ctypes.POINTER(GgufKv), ctypes.c_size_t, ctypes.POINTER(ctypes.c_int64)]),
 })
 
+
+
+# include/osmos/cpu/lane.h (host threads: the lane's CPU half touches no GPU)
+CPU_LANE_FAILED = 0x80000000
+
+
+class CpuLaneExpert(ctypes.Structure):
+    _fields_ = [("gate", P), ("up", P), ("down", P), ("row0", U32), ("cnt", U32)]
+
+
+class CpuLaneJob(ctypes.Structure):
+    _fields_ = [("type_gu", U32), ("type_down", U32), ("dim", U32), ("ff", U32), ("lim", F32), ("x", P),
+                ("scale", P), ("n_rows", U32), ("e", ctypes.POINTER(CpuLaneExpert)), ("n_e", U32), ("y", P),
+                ("seq", P), ("value", U32)]
+
+
+SIGS.update({
+    "cpu_lane_create": (P, [ctypes.c_int, P, U32, U32, U32]),
+    "cpu_lane_destroy": (None, [P]),
+    "cpu_lane_submit": (B, [P, ctypes.POINTER(CpuLaneJob)]),
+    "cpu_lane_wait": (B, [P]),
+})
+
 _lib = None
 
 

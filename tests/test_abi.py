@@ -21,7 +21,7 @@ def declared():
                 text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
                 text = re.sub(r"//[^\n]*", "", text)
                 text = re.sub(r"static inline[^{]*\{[^}]*\}", "", text, flags=re.S)
-                for m in re.finditer(r"^\s*(?:const\s+)?(?:bool|void|uint32_t|uint64_t|int|Gguf|GgufTensor|GgufKv)\s*\**\s*"
+                for m in re.finditer(r"^\s*(?:const\s+)?(?:bool|void|uint32_t|uint64_t|int|Gguf|GgufTensor|GgufKv|CpuLane)\s*\**\s*"
                                      r"([a-z_0-9]+)\s*\(", text, re.M):
                     names.add(m.group(1))
     return names
