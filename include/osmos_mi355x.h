@@ -82,4 +82,9 @@ bool osmos_lane_gate_up(const OsmosLaneLayer *layer, const float *x, uint32_t n_
 bool osmos_lane_down(const OsmosLaneLayer *layer, const float *h, uint32_t n_tok, const int32_t *ids, const float *add,
                      float *out, void *stream);
 
+/* ops_wait's bound (include/osmos/gpu/ops.h), in microseconds of wall clock, for the calls queued after this one; 0:
+   the default, ten minutes. no counterpart in the reference, whose wait has no bound: a stream can never be held for
+   good by a host that never posts, and a failure test can end a wait early on purpose */
+void osmos_wait_limit(uint64_t us);
+
 #endif

@@ -36,6 +36,7 @@ SIGS = {
     "q4x_moe_sum": (B, [P, P, P, U32, U32, U32, P, P, P, P]),
     "q4x_swiglu_rows": (B, [P, P, U32, P, U32, P, P, P]),
     "ops_wait": (B, [P, U32, P]),
+    "osmos_wait_limit": (None, [U64]),
     "ops_copy_rows": (B, [P, P, P, U32, U32, P]),
     "mm_known": (B, [U32]),
     "mm_fits": (B, [U32, U32, U32]),

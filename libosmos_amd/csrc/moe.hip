@@ -7,7 +7,10 @@
 // slots in whole tiles of 16, parts of at most 128 tokens in runs of 1/2/4/8 tiles; the sum: picks in order, then the
 // sigmoid-gated shared expert), reference include/osmos/gpu/ops.h:311-355 and kernels/ops.hip:502-525 (swiglu_lane,
 // gather_rows, gather_sum_add), reference src/run/hip_lane.c:115-200 (the lane's entries and token order).
+#include <atomic>
+
 #include "common.h"
+
 #include "x16.h"
 
 extern "C" {
@@ -205,27 +208,38 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(float* __restrict__ ds
   if (i < (uint64_t) n * len) dst[i] = src[(uint64_t) idx[i / len] * len + i % len];
 }
 
-// the stream held until *flag (host memory the GPU maps) holds value, or value with its top bit set (the host's mark of
+// the stream held until *flag (host memory the GPU maps) holds value, with or without its top bit (the host's mark of
 // a failed job) - one thread polling it with system-scope acquire loads (vector loads: never the scalar cache, which
-// would not see the host's store), a sleep between polls. the poll is bounded (2^32 polls of about 1.7 us: about two
-// hours) so the kernel always ends; the reference waits without bound (kernels/ops.hip:878-882)
-__global__ __launch_bounds__(64) void wait_kernel(const uint32_t* flag, uint32_t value) {
+// would not see the host's store), a sleep between polls. the wait is bounded by the wall clock (s_memrealtime's 100
+// MHz counter; the reference waits without bound, kernels/ops.hip:878-882): past `limit` ticks it gives up and sets
+// `expired`, which makes the next row copy write NaN rows rather than rows the host never wrote; a wait that ends
+// with the value clears it
+__device__ uint32_t expired = 0;
+__global__ __launch_bounds__(64) void wait_kernel(const uint32_t* flag, uint32_t value, uint64_t limit) {
   if (threadIdx.x) return;
-  const uint32_t marked = value | 0x80000000u;
-  for (uint32_t i = 0; i != 0xFFFFFFFFu; i++) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
     const uint32_t v = __hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-    if (v == value || v == marked) return;
+    if ((v & 0x7FFFFFFFu) == value) {
+      __hip_atomic_store(&expired, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+      __hip_atomic_store(&expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
     __builtin_amdgcn_s_sleep(64);
   }
 }
 
-// rows idx[0 .. n) of src copied to the same rows of dst, len floats a row (src may be mapped host memory)
+// rows idx[0 .. n) of src copied to the same rows of dst, len floats a row (src may be mapped host memory); NaN rows
+// instead after a wait that expired
 __global__ __launch_bounds__(256) void copy_rows_kernel(float* __restrict__ dst, const float* __restrict__ src,
                                                         const int32_t* __restrict__ idx, uint32_t n, uint32_t len) {
   const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
   if (i < (uint64_t) n * len) {
     const uint64_t at = (uint64_t) idx[i / len] * len + i % len;
-    dst[at] = src[at];
+    dst[at] = __hip_atomic_load(&expired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? __builtin_nanf("") : src[at];
   }
 }
 
@@ -402,9 +416,17 @@ extern "C" OSM_API bool ops_gather_rows(float* dst, const float* src, const int3
   return hipGetLastError() == hipSuccess;
 }
 
+namespace {
+std::atomic<uint64_t> wait_limit_ticks{600ull * 100000000ull};  // (ten minutes of the 100 MHz counter)
+}
+
+extern "C" OSM_API void osmos_wait_limit(uint64_t us) {
+  wait_limit_ticks.store(us ? us * 100ull : 600ull * 100000000ull, std::memory_order_relaxed);
+}
+
 extern "C" OSM_API bool ops_wait(const uint32_t* flag, uint32_t value, void* stream) {
-  if (!flag) return false;
-  moe::wait_kernel<<<1, 64, 0, (hipStream_t) stream>>>(flag, value);
+  if (!flag || (value & 0x80000000u)) return false;  // (a value with the failed mark's bit: not one a job posts)
+  moe::wait_kernel<<<1, 64, 0, (hipStream_t) stream>>>(flag, value, wait_limit_ticks.load(std::memory_order_relaxed));
   return hipGetLastError() == hipSuccess;
 }
 

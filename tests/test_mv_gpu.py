@@ -145,3 +145,30 @@ def test_mv_one_token_unaligned_matrix(g, name):
         print("mv_run one token", name, what, flush=True)
         g.call("mv_run", t, g.a(wt), rows, cols, g.a(xd), 1, g.a(y), None)
         assert (g.bits(g.host(y)) == g.bits(want)).all(), what
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "IQ1_M", "IQ1_S"])
+def test_mv_group_mixed_alignment(g, name):
+    """mv_group over the types whose rows the launch stages through LDS, at cols 2048 (a row a whole number of 16-byte
+    words): a table mixing 16-aligned matrices with ones that start 8 bytes past a 16-byte boundary, so one launch
+    takes the staged path for some matrices and the direct path for others - the oracle's bits for every matrix"""
+    import torch
+    t = synth.ID[name]
+    rows, cols, n = 70, 2048, 6
+    ws = [weights(name, rows, cols, 90 + m) for m in range(n)]
+    keep = []
+    for m, w in enumerate(ws):
+        b = w.size
+        buf = torch.zeros(b + 64, dtype=torch.uint8, device="cuda")
+        off = 8 if m % 2 else 0
+        buf[off:off + b] = torch.from_numpy(np.ascontiguousarray(w).reshape(-1)).cuda()
+        keep.append(buf[off:off + b])
+        assert keep[-1].data_ptr() % 16 == off
+    tab = g.table(keep)
+    x = np.random.default_rng(6).normal(0, 1, (n, cols)).astype(np.float32)
+    y = torch.full((n, rows), float("nan"), device="cuda")
+    print("mv_group mixed alignment", name, flush=True)
+    g.call("mv_group", t, g.a(tab), n, rows, cols, g.a(g.dev(x)), cols, 1, g.a(y), None)
+    yh = g.host(y)
+    for m in range(n):
+        assert (g.bits(yh[m]) == g.bits(orc.mv_rows(t, ws[m], rows, cols, x[m:m + 1])[0])).all(), m

@@ -60,3 +60,31 @@ def test_refusals():
     p = capi.ctypes.c_void_p(8)
     assert not L.ops_copy_rows(None, p, p, 1, 1, None)
     assert not L.ops_copy_rows(p, p, p, 0, 1, None) and not L.ops_copy_rows(p, p, p, 1, 0, None)
+
+
+def test_wait_bound_then_nan_rows():
+    """a flag the host never posts: with the bound set to 2 ms the wait ends by itself and the copy after it writes NaN
+    rows (not the host's unwritten ones); the next wait that sees its value makes copies copy again"""
+    import torch
+    L = capi.lib()
+    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    rows, n = 8, 64
+    src = torch.full((rows, n), 3.0, pin_memory=True)
+    dst = torch.zeros(rows, n, device="cuda")
+    idx = torch.tensor([1, 5], dtype=torch.int32, device="cuda")
+    print("ops_wait bound", flush=True)
+    L.osmos_wait_limit(2000)
+    try:
+        assert L.ops_wait(capi.addr(flag), 9, None)
+        assert L.ops_copy_rows(capi.addr(dst), capi.addr(src), capi.addr(idx), 2, n, None)
+        torch.cuda.synchronize()
+    finally:
+        L.osmos_wait_limit(0)
+    out = dst.cpu().numpy()
+    assert np.isnan(out[[1, 5]]).all() and (out[[0, 2, 3, 4, 6, 7]] == 0).all()
+    flag.fill_(9 - (1 << 31))  # 9 with the top bit set (a failed job), as a signed int32: still the post
+    assert L.ops_wait(capi.addr(flag), 9, None)
+    assert L.ops_copy_rows(capi.addr(dst), capi.addr(src), capi.addr(idx), 2, n, None)
+    torch.cuda.synchronize()
+    assert (dst.cpu().numpy()[[1, 5]] == 3.0).all()
+    assert not L.ops_wait(capi.addr(flag), 9 | (1 << 31), None)  # a value with the mark's bit: refused
