@@ -6,14 +6,16 @@
 // integer dot with the int8 activations, then ((d s21) / 8) isum per half, the halves added, fmaf'd with the block's
 // activation scale onto the lane's sum; then the lanes' xor tree (pairs ll, ll ^ L/2 first, then ll ^ L/4, ...).
 //
-// CDNA4 mapping: a workgroup owns 16 rows (their whole slab and the codebook staged in LDS once) x CT tiles of 16
+// CDNA4 mapping: a workgroup owns 16 rows (their whole slab and the codebook staged in LDS once) x G groups of 8
 // tokens a pass. the integer half-dots are MFMAs: each 32-value block's codes (lane l: row l % 16, values 8 (l / 16) ..
-// + 7, decoded from LDS straight into its B operand - the IQ1 types' 8 grid + delta folded into one int8 per value;
-// the tokens' codes the A operand) go to two v_mfma_i32_16x16x32_i8, one with the second half's lanes zeroed, one
-// with the first's: the two halves' exact dots, D[token][row] - lane l holds tokens 4 (l / 16) + i of its own row
-// l % 16, so it applies that row's half scales itself. the float steps then run per output in the contract's order. the 4 waves split
-// the logical lanes (wave w the chains ll = w mod 4, blocks s = w mod 4), so a wave keeps L / 4 chains an output in
-// registers; the xor tree is finished across the waves through LDS with the same additions (fadd commutes exactly).
+// + 7, decoded from LDS straight into its B operand - the IQ1 types' 8 grid + delta folded into one int8 per value)
+// against an A operand of 8 tokens' halves (row i: token i / 2's half i % 2, the other half's k zeroed), one
+// v_mfma_i32_16x16x32_i8 a group: lane l gets both half-dots of tokens 2 (l / 16), 2 (l / 16) + 1 for its row l % 16,
+// so it applies that row's half factors itself, the dots coming out of the MFMA as floats' bits (a bias in its
+// accumulator) so each product is one fma. the float steps then run per output in the contract's order. the W waves
+// split the logical lanes (wave w the chains ll = w mod W, blocks s = w mod W), so a wave keeps L / W chains an output
+// in registers; the xor tree is finished across the waves through LDS with the same additions (fadd commutes exactly).
+// groups of 8 tokens waste at most 7 token slots a matrix (prefill's many small experts).
 #include "lanedec.h"
 
 extern "C" {
@@ -67,11 +69,11 @@ __device__ inline void chunk<kIQ2_XXS>(lbytes b, int j, int k, const GridOf<kIQ2
                                        uint32_t& w0,
                                        uint32_t& w1) {
   const auto q = b + 2 + 8 * j;
-  signs8(grid[q[k]], sm[(ld32s(q + 4) >> (7 * k)) & 0x7F], w0, w1);
+  signs8(grid[q[k]], sm[(ld32b(q + 4) >> (7 * k)) & 0x7F], w0, w1);
 }
 template <>
 __device__ inline void scales<kIQ2_XXS>(lbytes b, int j, float& d, int& s0, int& s1) {
-  s0 = s1 = 2 * (int) (ld32s(b + 2 + 8 * j + 4) >> 28) + 1;
+  s0 = s1 = 2 * (int) (ld32b(b + 2 + 8 * j + 4) >> 28) + 1;
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:57-66
@@ -110,13 +112,13 @@ __device__ inline void chunk<kIQ3_XXS>(lbytes b, int j, int k, const GridOf<kIQ3
                                        uint32_t& w0,
                                        uint32_t& w1) {
   const auto q = b + 2 + 8 * j;
-  const uint32_t sg = (ld32s(b + 66 + 4 * j) >> (7 * k)) & 0x7F, par = __builtin_popcount(sg) & 1u;
+  const uint32_t sg = (ld32b(b + 66 + 4 * j) >> (7 * k)) & 0x7F, par = __builtin_popcount(sg) & 1u;
   w0 = grid[16 * q[2 * k] + (sg & 15)];
   w1 = grid[16 * q[2 * k + 1] + ((sg >> 4) | par << 3)];
 }
 template <>
 __device__ inline void scales<kIQ3_XXS>(lbytes b, int j, float& d, int& s0, int& s1) {
-  s0 = s1 = 2 * (2 * (int) (ld32s(b + 66 + 4 * j) >> 28) + 1);
+  s0 = s1 = 2 * (2 * (int) (ld32b(b + 66 + 4 * j) >> 28) + 1);
   d = f16(ld16(b));
 }
 // reference kernels/q8.h:120-130
@@ -156,51 +158,85 @@ __device__ inline void scales<kIQ1_M>(lbytes b, int j, float& d, int& s0, int& s
   d = f16((a0 >> 12) | ((a1 >> 8) & 0x00F0) | ((a2 >> 4) & 0x0F00) | (a3 & 0xF000));
 }
 
-// token tiles a pass and waves a workgroup at 16 / 32 logical lanes: the waves split the logical lanes, so a wave holds
-// L / W chains x CT tiles x 4 accumulators (64 / 32 VGPRs), and each decoded block serves CT tiles. measured on config
-// 5's IQ2_XXS gate (32 lanes): 4 waves and one tile 1.98 ms; 8 waves (so four tiles fit) 3.2 ms, 8 waves and two
-// tiles 2.2 ms - most of its experts hold one tile, and the larger workgroups halve the occupancy
-constexpr int kCT16 = 4, kCT32 = 1, kW16 = 4, kW32 = 4;
+// a block's two half factors, the contract's ((d s21) / 8) per half (lane_part's first two products)
+template <uint32_t T>
+__device__ inline void factors(lbytes b, int j, float& f0, float& f1) {
+  float d;
+  int s0, s1;
+  scales<T>(b, j, d, s0, s1);
+  f0 = __fmul_rn(__fmul_rn(d, (float) s0), 0.125f), f1 = __fmul_rn(__fmul_rn(d, (float) s1), 0.125f);
+}
+
+// the integer half-dots come out of the MFMA biased by kBias (its accumulator input): kBias + I as a float's bits is
+// 1.5 2^23 + I exactly for |I| < 2^22 (a half's dot is under 2^18: 16 codes of at most 127 x 62), so
+// fmaf(f, bits, -(f 1.5 2^23)) is f I rounded once - RN(f I), the contract's product, with no int-to-float convert.
+// (-(f 1.5 2^23) is exact: f has at most 17 significant bits. for a finite f; a block whose scale d is not finite
+// gives NaN there, where the contract's product is +-inf or NaN)
+constexpr int kBias = 0x4B400000;
+constexpr float kBiasF = 12582912.0f;
+
+// tokens an MFMA: the A operand's 16 rows are 8 tokens' two halves, row i token i / 2's half i % 2 (a first half's
+// values 0 .. 15 in the lanes of k 0 .. 15, zeros in those of k 16 .. 31; a second half's the other way round), the B
+// operand the block's full 32 codes of 16 weight rows: one MFMA gives both half-dots of 8 tokens x 16 rows, and lane l
+// holds D rows 4 (l / 16) .. + 3 of column l % 16 - both halves of tokens 2 (l / 16) and 2 (l / 16) + 1 of its row
+constexpr int kGroup = 8;
+// token groups a pass (G) and waves a workgroup (W) by type and lane count: the waves split the logical lanes, so a
+// wave holds L / W chains x G groups x 2 accumulators, and each decoded block serves G groups. measured on config 5's
+// routing (512 tokens, 250 experts, the busiest 441) at 2048 x 7168 (us): IQ2_XXS G/W 2/4 1609, 1/8 1320, 2/8 1355,
+// 4/8 1582, 2/16 1356; IQ3_XXS 2/4 3159, 2/8 1742, 4/8 1664, 2/16 1413, 1/16 1485; IQ1_M 2/4 2068, 2/8 1426, 2/16
+// 1472; at 7168 x 2048 (16 lanes) IQ2_XXS 2/4 1352, 4/4 1602, 8/4 2598, 2/8 1432. (IQ3_XXS's 16 KB signed codebook
+// and 44 KB slab leave room for two workgroups a CU: it wants the most waves)
+struct Shape {
+  int g, w;
+};
+template <uint32_t T, int L>
+constexpr Shape shape() {
+#ifdef OSM_LG  // (a build-time override, for tuning sweeps)
+  return L == 16 ? Shape{OSM_LG16, OSM_LW16} : Shape{OSM_LG32, OSM_LW32};
+#endif
+  if constexpr (L == 16) return {2, 4};
+  else if constexpr (T == kIQ3_XXS) return {2, 16};
+  else return {2, 8};
+}
 
 template <uint32_t T>
 constexpr uint32_t grid_bytes_of() {
   return GridOf<T>::n * sizeof(typename GridOf<T>::E);
 }
 
-// dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the sign masks, the waves' scale tables
-// and their partial trees
-template <uint32_t T, int CT, int W>
+// dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the sign masks, the waves' partial trees
+template <int G, int W>
 struct Lds {
   uint32_t slab, grid, sm, part, total;
-  __host__ __device__ Lds(uint32_t rb) {
+  __host__ __device__ Lds(uint32_t rb, uint32_t grid_bytes) {
     slab = 0;
     grid = (16 * rb + 15) / 16 * 16;
-    sm = grid + grid_bytes_of<T>();
+    sm = grid + grid_bytes;
     part = sm + 128 * 8;
-    total = part + W * CT * 4 * kWave * 4;
+    total = part + W * G * 2 * kWave * 4;
   }
 };
 
-// blockIdx.x: 16 rows; blockIdx.y: the matrix, its cnt[m] tokens from row xrow[m] of q / d, CT tiles of 16 a pass.
+// blockIdx.x: 16 rows; blockIdx.y: the matrix, its cnt[m] tokens from row xrow[m] of q / d, G groups of 8 a pass.
 // wave w takes the blocks s = w (mod W): its chains are the logical lanes ll = w (mod W), L / W accumulators an
 // output; the xor tree's levels L/2 .. W pair chains of one wave (in registers), its levels W/2 .. 1 pair the waves
 // (through LDS) - the same additions as the tree
-template <uint32_t T, int L, int CT, int W>
+template <uint32_t T, int L, int G, int W>
 __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
                                                    const int32_t* __restrict__ xrow, uint32_t cols,
                                                    const int8_t* __restrict__ q, const float* __restrict__ d,
                                                    float* __restrict__ y, uint32_t ys) {
-  constexpr int kWaves = W, kThreads = W * kWave;
-  constexpr int per = (int) (Block<T>::values / 32), C = L / kWaves;
+  constexpr int kThreads = W * kWave, per = (int) (Block<T>::values / 32), C = L / W, TOK = kGroup * G;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
   if (!n) return;  // (the whole workgroup)
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, col = lane % 16, quad = lane / 16;
+  // (the wave index through readfirstlane: uniform, so the block loop and its offsets are scalar)
+  const int wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / kWave)), lane = threadIdx.x % kWave;
+  const int col = lane % 16, quad = lane / 16;
   const uint32_t row0 = blockIdx.x * kTile, nblk = cols / 32, r0 = (uint32_t) xrow[m];
   const uint32_t rb = (uint32_t) row_bytes<T>(cols);
-  const Lds<T, CT, W> L_(rb);
-  // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
-  {
+  const Lds<G, W> L_(rb, grid_bytes_of<T>());
+  {  // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
     const u32x4* src = (const u32x4*) (w[m] + (uint64_t) row0 * rb);
     const uint32_t nw = 16 * rb / 16;
     for (uint32_t i = threadIdx.x; i < nw; i += kThreads) ((u32x4*) (smem + L_.slab))[i] = src[i];
@@ -209,124 +245,129 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
     for (uint32_t i = threadIdx.x; i < ng; i += kThreads) ((u32x4*) (smem + L_.grid))[i] = gs[i];
     if (threadIdx.x < 128) ((uint64_t*) (smem + L_.sm))[threadIdx.x] = sign_mask(threadIdx.x);
   }
-  __syncthreads();
   const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
   const uint64_t* sm = (const uint64_t*) (smem + L_.sm);
-  float* part = (float*) (smem + L_.part);                    // [wave][ct][i][lane]
-  const uint8_t* arow = smem + L_.slab + col * rb;            // this lane's A row
-  for (uint32_t c0 = 0; c0 < n; c0 += kTile * CT) {
-    // (the matrix's first token row as a scalar base, each lane's token as a 32-bit offset from it: tokens under
-    // OSMOS_LANE_MAX_TOKENS, so tt cols fits)
-    const int8_t* qb = q + (uint64_t) r0 * cols;
-    const float* db = d + (uint64_t) r0 * nblk;
-    uint32_t xb[CT], xd[CT];
+  float* part = (float*) (smem + L_.part);  // [wave][g][pair][lane]
+  const uint8_t* brow = smem + L_.slab + col * rb;  // this lane's B row (a weight row)
+  // the A operand's rows from a buffer descriptor over the matrix's token rows: a lane whose (row, k) is a zero of
+  // the layout, or whose token is past the count, reads at an offset past the descriptor's end - zeros, no access
+  const __amdgpu_buffer_rsrc_t qr =
+      __builtin_amdgcn_make_buffer_rsrc((void*) (q + (uint64_t) r0 * cols), (short) 0, 0x7FFFFFFF, 0x00020000);
+  // and the block scales of this lane's output tokens (a token past the count: zero, no access)
+  const __amdgpu_buffer_rsrc_t dr =
+      __builtin_amdgcn_make_buffer_rsrc((void*) (d + (uint64_t) r0 * nblk), (short) 0, 0x7FFFFFFF, 0x00020000);
+  const bool lives = (col % 2 == 0) == (quad < 2);
+  // this lane's two outputs of a group: tokens ot, ot + 1 of the group, row col
+  const int ot = 2 * quad;
+  v4i bias = {kBias, kBias, kBias, kBias};
+  asm volatile("" : "+v"(bias));  // (held in registers, not rebuilt before every MFMA)
+  for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
+    __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
+    const int groups = (int) ((n - c0 + kGroup - 1) / kGroup) < G ? (int) ((n - c0 + kGroup - 1) / kGroup) : G;
+    uint32_t voff[G], xoff[G][2];
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++) {  // this lane's B token (past the count: the last, summed, never stored)
-      const uint32_t t = c0 + ct * kTile + col, tt = t < n ? t : n - 1;
-      xb[ct] = tt * cols + 8 * quad;
-      xd[ct] = tt * nblk;
+    for (int g = 0; g < G; g++) {
+      const uint32_t t = c0 + g * kGroup + col / 2;
+      voff[g] = lives && t < n ? t * cols + 8 * quad : 0x80000000u;
+#pragma unroll
+      for (int p = 0; p < 2; p++) {
+        const uint32_t to = c0 + g * kGroup + ot + p;
+        xoff[g][p] = to < n ? to * nblk * 4 : 0x80000000u;
+      }
     }
-    const int tiles = (int) ((n - c0 + kTile - 1) / kTile) < CT ? (int) ((n - c0 + kTile - 1) / kTile) : CT;
-    float acc[C][CT][4];
+    float acc[C][G][2];
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
-      for (int ct = 0; ct < CT; ct++)
+      for (int g = 0; g < G; g++) acc[c][g][0] = acc[c][g][1] = 0.0f;
+    // the A words and token scales of the wave's next block, loaded one block ahead
+    long an[G];
+    float xn[G][2];
+    auto aload = [&](uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[c][ct][i] = 0.0f;
-    // the activations of the wave's next block, loaded one block ahead (global memory's latency behind the MFMAs)
-    long bxn[CT];
-    float xsn[CT];
-    auto xload = [&](uint32_t s) __attribute__((always_inline)) {
+      for (int g = 0; g < G; g++)
+        if (g < groups) {
+          an[g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
 #pragma unroll
-      for (int ct = 0; ct < CT; ct++) {
-        const uint32_t sc = s < nblk ? s : 0;
-        bxn[ct] = *(const long*) (qb + (xb[ct] + sc * 32));
-        xsn[ct] = db[xd[ct] + sc];
-      }
+          for (int p = 0; p < 2; p++)
+            xn[g][p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff[g][p], s * 4, 0));
+        }
     };
-    xload((uint32_t) wave);
+    aload((uint32_t) wave);
     for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += L) {
 #pragma unroll
       for (int c = 0; c < C; c++) {
-        const uint32_t s = s0 + kWaves * c;  // logical lane wave + 4 c
-        if (s >= nblk) break;                // (uniform)
-        long bx[CT];
-        float xs[CT];
+        const uint32_t s = s0 + W * c;  // logical lane wave + W c
+        if (s >= nblk) break;           // (uniform)
+        long a[G];
+        float x[G][2];
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) bx[ct] = bxn[ct], xs[ct] = xsn[ct];
-        xload(s + kWaves);
-        const uint8_t* blk = arow + (s / per) * Block<T>::bytes;
+        for (int g = 0; g < G; g++) a[g] = an[g], x[g][0] = xn[g][0], x[g][1] = xn[g][1];
+        aload(s + W < nblk ? s + W : s);  // (the last block: loaded again, unused - no branch)
+        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
         const int j = (int) (s % per);
         uint32_t w0, w1;
         chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
-        const long a = (long) (((uint64_t) w1 << 32) | w0);
-        const long a0 = quad < 2 ? a : 0, a1 = quad < 2 ? 0 : a;  // the first half's lanes, the second's
-        // row col's ((d s21) / 8) per half (lane_part's first two products): every lane its own row's
-        float dd;
-        int s0_, s1_;
-        scales<T>((lbytes) blk, j, dd, s0_, s1_);
-        const float f0 = __fmul_rn(__fmul_rn(dd, (float) s0_), 0.125f), f1 = __fmul_rn(__fmul_rn(dd, (float) s1_), 0.125f);
+        const long b = (long) (((uint64_t) w1 << 32) | w0);
+        float f0, f1;
+        factors<T>((lbytes) blk, j, f0, f1);
+        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) {
-          if (ct < tiles) {
-            // tokens the A operand, weight rows the B: D[token 4 quad + i][row col]
-            const v4i I0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(bx[ct], a0, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const v4i I1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(bx[ct], a1, v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              // token 4 quad + i's block scale, from the lane that loaded it (lane 4 quad + i: token col)
-              const float xt = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * quad + i) * 4, __float_as_int(xs[ct])));
-              const float sub = __fadd_rn(__fmul_rn(f0, (float) I0[i]), __fmul_rn(f1, (float) I1[i]));
-              acc[c][ct][i] = __builtin_fmaf(xt, sub, acc[c][ct][i]);
-            }
+        for (int g = 0; g < G; g++) {
+          if (g < groups) {
+            const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[g], b, bias, 0, 0, 0);
+            const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0),
+                                        __builtin_fmaf(f1, __int_as_float(D[1]), n1));
+            const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0),
+                                        __builtin_fmaf(f1, __int_as_float(D[3]), n1));
+            acc[c][g][0] = __builtin_fmaf(x[g][0], s0_, acc[c][g][0]);
+            acc[c][g][1] = __builtin_fmaf(x[g][1], s1_, acc[c][g][1]);
           }
         }
       }
     }
-    // the tree's levels L/2 .. 4 within the wave: chains c and c ^ o4 (logical lanes ll and ll ^ 4 o4)
+    // the tree's levels L/2 .. W within the wave: chains c and c + o (logical lanes ll and ll ^ W o)
 #pragma unroll
-    for (int o4 = C / 2; o4 > 0; o4 >>= 1)
+    for (int o = C / 2; o > 0; o >>= 1)
 #pragma unroll
-      for (int c = 0; c < o4; c++)
+      for (int c = 0; c < o; c++)
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[c][ct][i] = __fadd_rn(acc[c][ct][i], acc[c + o4][ct][i]);
+          for (int p = 0; p < 2; p++) acc[c][g][p] = __fadd_rn(acc[c][g][p], acc[c + o][g][p]);
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) part[((wave * CT + ct) * 4 + i) * kWave + lane] = acc[0][ct][i];
+      for (int p = 0; p < 2; p++) part[((wave * G + g) * 2 + p) * kWave + lane] = acc[0][g][p];
     __syncthreads();
     // levels W/2 .. 1 across the waves (T_w: wave w's subtree, logical lanes w mod W): each pass pairs w with
-    // w + o for w < o, as the tree pairs logical lanes ll and ll ^ o. the CT 4 outputs of a lane are shared out
-    // over the waves: wave v finishes outputs v, v + W, ...
+    // w + o for w < o, as the tree pairs logical lanes ll and ll ^ o. a lane's 2 G outputs are shared out over the
+    // waves: wave v finishes outputs v, v + W, ...
     {
-      const uint32_t wv = CT * 4 * kWave;  // a wave's stride
-      for (int oi = (int) wave; oi < CT * 4; oi += kWaves) {
-        const int ct = oi / 4, i = oi % 4;
-        const float* pp = part + (ct * 4 + i) * kWave + lane;
-        float t[kWaves];
+      const uint32_t wv = G * 2 * kWave;  // a wave's stride
+      for (int oi = (int) wave; oi < G * 2; oi += W) {
+        const int g = oi / 2, p = oi % 2;
+        const float* pp = part + (g * 2 + p) * kWave + lane;
+        float t[W];
 #pragma unroll
-        for (int v = 0; v < kWaves; v++) t[v] = pp[v * wv];
+        for (int v = 0; v < W; v++) t[v] = pp[v * wv];
 #pragma unroll
-        for (int o = kWaves / 2; o > 0; o >>= 1)
+        for (int o = W / 2; o > 0; o >>= 1)
 #pragma unroll
           for (int v = 0; v < o; v++) t[v] = __fadd_rn(t[v], t[v + o]);
-        const uint32_t tk = c0 + ct * kTile + 4 * quad + i;  // (D: token 4 quad + i, row col)
+        const uint32_t tk = c0 + g * kGroup + ot + p;
         if (tk < n) y[(uint64_t) (r0 + tk) * ys + row0 + col] = t[0];
       }
     }
-    __syncthreads();  // the partial trees read before the next pass writes them
   }
 }
 
-template <uint32_t T, int L, int CT, int W>
+template <uint32_t T, int L, int G, int W>
 bool launch(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t rows,
             uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
-  const Lds<T, CT, W> l((uint32_t) row_bytes<T>(cols));
+  const Lds<G, W> l((uint32_t) row_bytes<T>(cols), grid_bytes_of<T>());
   if (l.total > 160 * 1024) return false;
-  auto k = kernel<T, L, CT, W>;
+  auto k = kernel<T, L, G, W>;
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
@@ -339,8 +380,9 @@ bool by_lanes(const void* const* w, const int32_t* cnt, const int32_t* xrow, uin
               uint32_t rows, uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
   if (cols % Block<T>::values) return false;
   (void) max_cnt;
-  return cols >= 4096 ? launch<T, 32, kCT32, kW32>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s)
-                      : launch<T, 16, kCT16, kW16>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s);
+  constexpr Shape s32 = shape<T, 32>(), s16 = shape<T, 16>();
+  return cols >= 4096 ? launch<T, 32, s32.g, s32.w>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s)
+                      : launch<T, 16, s16.g, s16.w>(w, cnt, xrow, n_mat, rows, cols, q, d, y, ys, s);
 }
 
 }  // namespace lgemm

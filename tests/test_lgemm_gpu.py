@@ -50,8 +50,8 @@ def test_lane_group_oracle(g, name, cols):
 
 
 def test_lane_group_invariance_and_drop_in(g):
-    """one matrix at 70 tokens (5 tiles: CT 2 passes) against the same tokens one at a time, and q8_group_tok's bits
-    at 8 tokens"""
+    """one matrix at 70 tokens (9 groups of 8 over 5 passes, the last group of 6) against the same tokens one at a time,
+    and q8_group_tok's bits at 8 tokens"""
     import torch
     name, rows, cols = "IQ2_XXS", 64, 2048
     t = synth.ID[name]
@@ -67,6 +67,24 @@ def test_lane_group_invariance_and_drop_in(g):
            g.a(g.dev(np.array([0], np.int32))), None, 1, 8, rows, cols, g.a(g.dev(q[:8])), g.a(g.dev(d[:8])), g.a(y8),
            rows, None)
     assert (g.bits(g.host(y8)) == g.bits(y[:8])).all()
+
+
+@pytest.mark.parametrize("cols", [512, 4096])
+def test_lane_group_nonfinite_scale(g, cols):
+    """a block whose f16 scale is +inf (no quantizer writes one): the rows of finite blocks keep the oracle's bits; a
+    row holding the inf block is NaN for every token (the integer dots come out of the MFMA biased, and the bias's
+    correction is inf - inf there), where the contract's own sums are +-inf or NaN"""
+    name, rows = "IQ2_XXS", 32
+    t = synth.ID[name]
+    w = synth.iq_blocks(t, rows, cols, 8)
+    w[5, 0:2] = np.frombuffer(np.float16(np.inf).tobytes(), np.uint8)  # row 5's first block scale
+    x = np.random.default_rng(3).normal(0, 1, (9, cols)).astype(np.float32)
+    q, d = orc.q8_round(x)
+    y, _ = run(g, t, [w], [9], rows, cols, q, d)
+    want = orc.q8_rows(t, w, rows, cols, q, d)
+    keep = [r for r in range(rows) if r != 5]
+    assert (g.bits(y[:9, keep]) == g.bits(want[:, keep])).all()
+    assert np.isnan(y[:9, 5]).all() and not np.isfinite(want[:, 5]).any()
 
 
 def test_lane_group_refusals(g):
