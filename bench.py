@@ -133,7 +133,8 @@ def gemv_extras(torch, capi):
             us = graph_us(torch, lambda i, st: L.mv_strided(t, capi.addr(W[i]), rows, cols, capi.addr(x), cols, n,
                                                             capi.addr(y), rows, st), G)
             nb = wbytes + n * cols * 4 + n * rows * 4
-            out["%s_%dx%d_mv_f32_bs%d" % (name, cols, rows, n)] = {"us": round(us, 3), "GB/s": round(nb / us / 1e3, 1)}
+            out["%s_%dx%d_mv_f32_bs%d" % (name, cols, rows, n)] = {"us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                                                                  "contract": "mv fp32 (the reference's bits)"}
             if n <= 8:
                 q = torch.zeros(n, cols, dtype=torch.int8, device="cuda")
                 d = torch.zeros(n, cols // 32, device="cuda")
@@ -145,8 +146,9 @@ def gemv_extras(torch, capi):
                                                                   capi.addr(xrow), None, 1, n, rows, cols, capi.addr(q),
                                                                   capi.addr(d), capi.addr(y), rows, st), G)
                 nb = wbytes + n * (cols + cols // 32 * 4) + n * rows * 4
-                out["%s_%dx%d_lane_int8_bs%d" % (name, cols, rows, n)] = {"us": round(us, 3),
-                                                                         "GB/s": round(nb / us / 1e3, 1)}
+                out["%s_%dx%d_lane_int8_bs%d" % (name, cols, rows, n)] = {
+                    "us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                    "contract": "lane int8, build-defined for %s (the reference's lane has no %s contract)" % (name, name)}
             if n >= 8:
                 x16 = torch.zeros((n + 15) // 16 * 16 * cols, dtype=torch.float16, device="cuda")
                 assert L.mm_x16(capi.addr(x), cols, n, cols, capi.addr(x16), None, None)
@@ -155,7 +157,8 @@ def gemv_extras(torch, capi):
                 nb = wbytes + n * cols * 2 + n * rows * 4
                 out["%s_%dx%d_mm_f16_bs%d" % (name, cols, rows, n)] = {
                     "us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
-                    "TFLOP/s": round(2 * rows * cols * n / us / 1e6, 2)}
+                    "TFLOP/s": round(2 * rows * cols * n / us / 1e6, 2),
+                    "contract": "mm f16 (the reference's K split, within its bound)"}
         del W
         torch.cuda.empty_cache()
     return out
