@@ -202,6 +202,11 @@ def deepseek_extras(torch, capi, steps=256):
     return out
 
 
+def roof_frac(us, nbytes, ops, peak_t):
+    """the config's roofline time, max(bytes / HBM peak, ops / MFMA peak), over the measured time"""
+    return round(max(nbytes / (HBM_PEAK_GBS * 1e3), ops / (peak_t * 1e6)) / us, 4)
+
+
 def prefill_extras(torch, capi):
     """config 5: 512 tokens routed top-8 over 256 experts with Zipf(1.1) load, each expert's tokens gathered in whole
     tiles: Q4_K down (2048 -> 7168) on the int8 matrix cores (mmq_group, its x8 beforehand) and IQ2_XXS gate
@@ -250,8 +255,11 @@ def prefill_extras(torch, capi):
                                                    cols, capi.addr(x8), capi.addr(dx), capi.addr(sx),
                                                    capi.addr(soff_d), capi.addr(y), capi.addr(yoff_d), rows, st), 4)
     tops = 2.0 * rows * cols * pairs_n / us / 1e6
+    nbytes = int((cnt > 0).sum()) * rows * (cols // 256) * 144 + slots * cols * 9 // 8 + pairs_n * rows * 4
     out["prefill_q4k_down_mmq_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
-                                        "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
+                                        "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
+                                        "roofline_frac": roof_frac(us, nbytes, 2.0 * rows * cols * pairs_n,
+                                                                   INT8_PEAK_TOPS)}
     # the dense sub-shape: one Q4_K expert 2048 -> 7168 over all 512 tokens (32 full tiles: no padded slots) - the
     # compute-bound case of the same kernel
     idx1 = torch.arange(n_tok, dtype=torch.int32, device="cuda")
@@ -267,8 +275,10 @@ def prefill_extras(torch, capi):
                                                    capi.addr(x8d), capi.addr(dxd), capi.addr(sxd), capi.addr(z),
                                                    capi.addr(yd), capi.addr(z), rows, st), 8)
     tops = 2.0 * rows * cols * n_tok / us / 1e6
-    out["dense_q4k_down_mmq_int8_512tok"] = {"us": round(us, 2), "TOPS": round(tops, 2),
-                                             "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
+    out["dense_q4k_down_mmq_int8_512tok"] = {
+        "us": round(us, 2), "TOPS": round(tops, 2), "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
+        "roofline_frac": roof_frac(us, rows * (cols // 256) * 144 + n_tok * cols * 9 // 8 + n_tok * rows * 4,
+                                   2.0 * rows * cols * n_tok, INT8_PEAK_TOPS)}
     del W, wt, x8, dx, sx, y, x8d, dxd, sxd, yd
     torch.cuda.empty_cache()
     # IQ2_XXS gate on f16 MFMA: rows 2048, cols 7168
@@ -285,8 +295,11 @@ def prefill_extras(torch, capi):
                                                   cols, capi.addr(x16), capi.addr(xoff_d), cols, capi.addr(y),
                                                   capi.addr(yoff_d), rows, st), 4)
     tf = 2.0 * rows * cols * pairs_n / us / 1e6
+    wbytes = int((cnt > 0).sum()) * rows * (cols // 256) * 66
     out["prefill_iq2xxs_gate_mm_f16"] = {"us": round(us, 1), "TFLOP/s": round(tf, 2),
-                                         "pct_f16_mfma_peak": round(100 * tf / F16_PEAK_TFLOPS, 3)}
+                                         "pct_f16_mfma_peak": round(100 * tf / F16_PEAK_TFLOPS, 3),
+                                         "roofline_frac": roof_frac(us, wbytes + slots * cols * 2 + pairs_n * rows * 4,
+                                                                    2.0 * rows * cols * pairs_n, F16_PEAK_TFLOPS)}
     # the same gate on the int8 matrix cores under the lane contract (the reference CPU lane's bits): each expert's
     # tokens gathered in order, rounded (q8_round), then osmos_lane_group
     order = [t for e in range(n_exp) for t in pairs[e]]
@@ -301,7 +314,10 @@ def prefill_extras(torch, capi):
                                                           capi.addr(y), rows, st), 4)
     tops = 2.0 * rows * cols * pairs_n / us / 1e6
     out["prefill_iq2xxs_gate_lane_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
-                                            "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3)}
+                                            "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
+                                            "roofline_frac": roof_frac(us, wbytes + pairs_n * cols * 9 // 8
+                                                                       + pairs_n * rows * 4,
+                                                                       2.0 * rows * cols * pairs_n, INT8_PEAK_TOPS)}
     del W, wt, x16, y
     torch.cuda.empty_cache()
     return out
@@ -455,6 +471,15 @@ def cpu_baseline(lay, seconds=10.0):
         t0 = time.perf_counter()
         assert R.ref_lane_layer_mt(*args, reps)
         per = (time.perf_counter() - t0) / reps
+        # one core as well (the same layer, a quarter of the sample's time)
+        args1 = args[:-1] + (1,)
+        t0 = time.perf_counter()
+        assert R.ref_lane_layer_mt(*args1, 1)
+        per1 = time.perf_counter() - t0
+        reps1 = max(2, int(seconds / 4 / max(per1, 1e-6)))
+        t0 = time.perf_counter()
+        assert R.ref_lane_layer_mt(*args1, reps1)
+        per1 = (time.perf_counter() - t0) / reps1
     else:
         threads = 1
         t0 = time.perf_counter()
@@ -467,9 +492,13 @@ def cpu_baseline(lay, seconds=10.0):
         per = (time.perf_counter() - t0) / reps
     del torch
     step_bytes = len(experts) * lay["per_expert"] + n_tok * dim * 8
-    return {"value": round(step_bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": "%d x one %d-token step of the same layer (%d experts' gate/up/down, int8 lane), %.2f ms a step"
-                      % (reps, n_tok, len(experts), per * 1e3)}
+    out = {"value": round(step_bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+           "sample": "%d x one %d-token step of the same layer (%d experts' gate/up/down, int8 lane), %.2f ms a step"
+                     % (reps, n_tok, len(experts), per * 1e3)}
+    if kind == "reference":
+        out["one_core"] = {"value": round(step_bytes / per1 / 1e9, 3), "unit": "GB/s",
+                           "sample": "%d x the same step on one thread, %.2f ms a step" % (reps1, per1 * 1e3)}
+    return out
 
 
 def ceilings(torch):
