@@ -26,6 +26,7 @@ __constant__ DecodeTables kDec = make_decode_tables();
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kTile = kX16Tile, kStep = 32;
 
@@ -40,12 +41,48 @@ struct Args {
   float* y;
 };
 
-// the codebook a type's decoder reads (Dec<T>::run's `tables`), held in LDS: only the members that type reads
+// the IQ2 / IQ3 grids as f16 (each grid byte's value as f16 bits) and the 8-value sign masks as f16 sign bits
+// (0x8000 in each negated value): sign7 by a 7-bit sign index (its parity bit folded in, gguf's ksigns), sign8 by
+// the 8 sign bits themselves
+constexpr uint16_t half_bits(uint32_t n) {  // a small positive integer's f16 bits
+  int e = 0;
+  while ((n >> (e + 1)) != 0) e++;
+  return (uint16_t) ((15 + e) << 10 | ((n << (10 - e)) & 0x3FFu));
+}
+struct alignas(16) HalfGrids {
+  uint16_t iq2xxs[256][8], iq2xs[512][8], iq2s[1024][8], iq3xxs[256][4], sign7[128][8], sign8[256][8];
+};
+constexpr HalfGrids make_half_grids() {
+  const Grids g = make_grids();
+  HalfGrids h{};
+  for (int i = 0; i < 256; i++)
+    for (int j = 0; j < 8; j++) h.iq2xxs[i][j] = half_bits((uint32_t) (g.iq2xxs[i] >> (8 * j)) & 0xFF);
+  for (int i = 0; i < 512; i++)
+    for (int j = 0; j < 8; j++) h.iq2xs[i][j] = half_bits((uint32_t) (g.iq2xs[i] >> (8 * j)) & 0xFF);
+  for (int i = 0; i < 1024; i++)
+    for (int j = 0; j < 8; j++) h.iq2s[i][j] = half_bits((uint32_t) (g.iq2s[i] >> (8 * j)) & 0xFF);
+  for (int i = 0; i < 256; i++)
+    for (int j = 0; j < 4; j++) h.iq3xxs[i][j] = half_bits((g.iq3xxs[i] >> (8 * j)) & 0xFF);
+  for (int i = 0; i < 256; i++) {
+    int par = 0;
+    for (int j = 0; j < 7; j++) par ^= (i >> j) & 1;
+    const int s7 = (i & 127) | par << 7;
+    for (int j = 0; j < 8; j++) {
+      if (i < 128) h.sign7[i][j] = (uint16_t) (((s7 >> j) & 1) << 15);
+      h.sign8[i][j] = (uint16_t) (((i >> j) & 1) << 15);
+    }
+  }
+  return h;
+}
+__constant__ HalfGrids kHalf = make_half_grids();
+
+// the codebook a type's decoder reads, held in LDS: for the generic decoder (decode.h's Layout<T>::at `tables`) only
+// the members that type reads; for the f16 path of the IQ2 / IQ3 types (decode_h below) the f16 grid and sign masks
 template <uint32_t T> struct LdsTab { struct { } g; };
-template <> struct LdsTab<kIQ2_XXS> { struct { uint64_t iq2xxs[256]; } g; };
-template <> struct LdsTab<kIQ2_XS> { struct { uint64_t iq2xs[512]; } g; };
-template <> struct LdsTab<kIQ2_S> { struct { uint64_t iq2s[1024]; } g; };
-template <> struct LdsTab<kIQ3_XXS> { struct { uint32_t iq3xxs[256]; } g; };
+template <> struct LdsTab<kIQ2_XXS> { uint16_t grid[256][8], sign[128][8]; };
+template <> struct LdsTab<kIQ2_XS> { uint16_t grid[512][8], sign[128][8]; };
+template <> struct LdsTab<kIQ2_S> { uint16_t grid[1024][8], sign[256][8]; };
+template <> struct LdsTab<kIQ3_XXS> { uint16_t grid[256][4], sign[128][8]; };
 template <> struct LdsTab<kIQ1_S> { struct { uint64_t iq1s[2048]; } g; };
 template <> struct LdsTab<kIQ1_M> { struct { uint64_t iq1s[2048]; } g; };
 template <> struct LdsTab<kIQ4_NL> { struct { } g; alignas(4) int8_t iq4nl[16]; };
@@ -54,15 +91,72 @@ template <> struct LdsTab<kIQ4_XS> { struct { } g; alignas(4) int8_t iq4nl[16]; 
 template <uint32_t T>
 __device__ inline void fill_tab(LdsTab<T>& t) {  // every thread of the workgroup, from the constant tables
   const uint32_t* src = nullptr;
-  uint32_t words = 0;
+  const uint32_t* src2 = nullptr;
+  uint32_t words = 0, words2 = 0;
   uint32_t* dst = (uint32_t*) &t;
-  if constexpr (T == kIQ2_XXS) src = (const uint32_t*) kDec.g.iq2xxs, words = sizeof t / 4;
-  else if constexpr (T == kIQ2_XS) src = (const uint32_t*) kDec.g.iq2xs, words = sizeof t / 4;
-  else if constexpr (T == kIQ2_S) src = (const uint32_t*) kDec.g.iq2s, words = sizeof t / 4;
-  else if constexpr (T == kIQ3_XXS) src = (const uint32_t*) kDec.g.iq3xxs, words = sizeof t / 4;
-  else if constexpr (T == kIQ1_S || T == kIQ1_M) src = (const uint32_t*) kDec.g.iq1s, words = sizeof t / 4;
+  uint32_t* dst2 = nullptr;
+  if constexpr (T == kIQ2_XXS || T == kIQ2_XS || T == kIQ2_S || T == kIQ3_XXS) {
+    if constexpr (T == kIQ2_XXS) src = (const uint32_t*) kHalf.iq2xxs;
+    else if constexpr (T == kIQ2_XS) src = (const uint32_t*) kHalf.iq2xs;
+    else if constexpr (T == kIQ2_S) src = (const uint32_t*) kHalf.iq2s;
+    else src = (const uint32_t*) kHalf.iq3xxs;
+    src2 = T == kIQ2_S ? (const uint32_t*) kHalf.sign8 : (const uint32_t*) kHalf.sign7;
+    words = sizeof t.grid / 4, words2 = sizeof t.sign / 4, dst = (uint32_t*) t.grid, dst2 = (uint32_t*) t.sign;
+  } else if constexpr (T == kIQ1_S || T == kIQ1_M) src = (const uint32_t*) kDec.g.iq1s, words = sizeof t / 4;
   else if constexpr (T == kIQ4_NL || T == kIQ4_XS) src = (const uint32_t*) kDec.iq4nl, words = 4, dst = (uint32_t*) t.iq4nl;
   for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) dst[i] = src[i];
+  for (uint32_t i = threadIdx.x; i < words2; i += blockDim.x) dst2[i] = src2[i];
+}
+
+// the IQ2 / IQ3 types straight to f16: their values are (scale) x (+-grid byte) with the product exact in F32
+// (scale d (0.5 + s) / 4 or / 2: at most 16 significant bits; a grid byte at most 6), so each value is the f16 grid
+// byte, its sign bit xored in, times the F32 scale and rounded once to f16 - decode.h's exact value rounded to f16,
+// the same bits, with no integer-to-float step
+template <uint32_t T>
+constexpr bool half_path() {
+  return T == kIQ2_XXS || T == kIQ2_XS || T == kIQ2_S || T == kIQ3_XXS;
+}
+template <uint32_t T>
+__device__ inline half8 decode_h(const LdsTab<T>& t, const uint8_t* b, int k) {
+  uint4 g, sg;
+  float scale;
+  if constexpr (T == kIQ2_XXS) {
+    const uint8_t* g8 = b + 2 + 8 * (k >> 2);
+    const uint32_t aux = ld32(g8 + 4);
+    scale = mul(mul(half_at(b), 0.5f + (float) (aux >> 28)), 0.25f);
+    g = *(const uint4*) t.grid[g8[k & 3]], sg = *(const uint4*) t.sign[(aux >> (7 * (k & 3))) & 127u];
+  } else if constexpr (T == kIQ2_XS) {
+    const uint32_t e = ld16(b + 2 + 2 * k), s = (b[66 + (k >> 2)] >> (4 * ((k >> 1) & 1))) & 15u;
+    scale = mul(mul(half_at(b), 0.5f + (float) s), 0.25f);
+    g = *(const uint4*) t.grid[e & 511u], sg = *(const uint4*) t.sign[e >> 9];
+  } else if constexpr (T == kIQ2_S) {
+    const uint32_t s = (b[74 + (k >> 2)] >> (4 * ((k >> 1) & 1))) & 15u;
+    const uint32_t idx = b[2 + k] | ((b[66 + (k >> 2)] >> (2 * (k & 3))) & 3u) << 8;
+    scale = mul(mul(half_at(b), 0.5f + (float) s), 0.25f);
+    g = *(const uint4*) t.grid[idx], sg = *(const uint4*) t.sign[b[34 + k]];
+  } else {  // IQ3_XXS: two 4-value grid entries a chunk
+    const uint8_t* idx = b + 2 + 2 * k;
+    const uint32_t aux = ld32(b + 66 + 4 * (k >> 2));
+    scale = mul(mul(half_at(b), 0.5f + (float) (aux >> 28)), 0.5f);
+    const uint2 g0 = *(const uint2*) t.grid[idx[0]], g1 = *(const uint2*) t.grid[idx[1]];
+    g = uint4{g0.x, g0.y, g1.x, g1.y}, sg = *(const uint4*) t.sign[(aux >> (7 * (k & 3))) & 127u];
+  }
+  const uint32_t w[4] = {g.x ^ sg.x, g.y ^ sg.y, g.z ^ sg.z, g.w ^ sg.w};
+  // each word's two values times the scale, rounded to f16 into the low and the high half of one register (the mixed
+  // fma: an F32 and an f16 operand, exact product, plus -0 so that a -0 product stays -0, one rounding to f16; the
+  // low form keeps the high half and the high form the low one, so the pair needs no packing)
+  uint32_t p[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#if __HIP_DEVICE_COMPILE__  // (the instruction exists on the device only; the host pass never runs this)
+    asm("v_fma_mixlo_f16 %0, %1, %2, neg(0) op_sel_hi:[0,1,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, %2, neg(0) op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+        : "=&v"(p[i])
+        : "v"(scale), "v"(w[i]));
+#else
+    p[i] = w[i] ^ __float_as_uint(scale);
+#endif
+  return __builtin_bit_cast(half8, u32x4{p[0], p[1], p[2], p[3]});
 }
 
 // a type's K split (reference kernels/mm.hip:24-73, the Tuned / Short / Odd shapes): SL values a slab, W partitions.
@@ -174,12 +268,16 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
           const uint8_t* row = smem + buf * kRows * kRb + (rt * kTile + lane % 16) * kRb;
-          float v[kChunk];
           int k;
           const uint8_t* b = chunk_at<T>(row, (wave * SL + k0) / kChunk + q, &k);
-          decode<T>(tab, b, k, v);
+          if constexpr (half_path<T>()) {
+            av[rt] = decode_h<T>(tab, b, k);
+          } else {
+            float v[kChunk];
+            decode<T>(tab, b, k, v);
 #pragma unroll
-          for (int i = 0; i < kChunk; i++) av[rt][i] = (_Float16) v[i];  // nearest, ties to even
+            for (int i = 0; i < kChunk; i++) av[rt][i] = (_Float16) v[i];  // nearest, ties to even
+          }
         }
         const uint32_t kk = k_slab + k0;
 #pragma unroll
