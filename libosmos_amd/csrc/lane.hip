@@ -63,6 +63,98 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   }
 }
 
+// one token (q8_group_tok at max_cnt 1, the decode GEMV): a row a group of 2L lanes (a half-wave at 16 logical lanes,
+// a wave at 32) - twice the lanes a row of group_tok_kernel, so twice the waves in flight. logical lane ll's chain
+// (blocks ll, ll + L, ... in order) is split: lane ll of the group's first half sums its first links' blocks and runs
+// them, lane ll of the second half sums the rest, takes the first's acc and finishes the chain; then the tree over
+// the second half - the contract's links in its order. STG: the group first copies its row into its own LDS slot with
+// 16-byte loads (a row whose bytes are a whole number of 16-byte words, at most kOneStg, the matrix 16-aligned) and
+// decodes from there: a row's bytes in a few wide loads instead of a block's header and codes in small pieces
+constexpr uint32_t kOneStg = 4608;  // a slot's bytes (Q4_K at 8192 columns)
+template <int L> struct OneShape {
+  static constexpr int group = 2 * L, rows = kThreads / group;  // a row's lanes, a workgroup's rows
+};
+// the types it serves and those it stages: measured on config 2's 2048 -> 6144 and config 1's 2048 -> 8192 at one
+// token (us, group_tok_kernel / one_kernel direct / one_kernel staged): Q4_K 8.49 / - / 7.87, Q3_K 7.49 / 6.68 / 8.25,
+// Q4_0 5.97 / 6.36 / 8.97 (Q4_0 stays with group_tok_kernel)
+template <uint32_t T> constexpr bool one_serves() { return T == kQ4_K || T == kQ3_K; }
+template <uint32_t T> constexpr bool one_stages() { return T == kQ4_K; }
+
+template <uint32_t T, int L, bool STG>
+__device__ __forceinline__ void one_row(const uint8_t* wm, uint32_t row, uint32_t r0, const int32_t* __restrict__ xin,
+                                        uint32_t cols, const int8_t* __restrict__ q, const float* __restrict__ d,
+                                        float* __restrict__ y, uint32_t ys) {
+  constexpr int GL = OneShape<L>::group, per = (int) (Block<T>::values / 32);
+  const int gl = threadIdx.x % GL, half = gl / L, ll = gl % L;
+  const uint32_t nblk = cols / 32;
+  const uint64_t rb = row_bytes<T>(cols);
+  const uint8_t* base = wm + (uint64_t) row * rb;
+  if constexpr (STG) {
+    __shared__ __attribute__((aligned(16))) uint8_t stg[OneShape<L>::rows][kOneStg];
+    uint8_t* slot = stg[threadIdx.x / GL];
+    const uint32_t words = (uint32_t) (rb / 16);
+    const uint4* src = (const uint4*) base;
+    constexpr int kMax = (int) (kOneStg / 16 + GL - 1) / GL;
+    uint4 r[kMax];
+#pragma unroll
+    for (int i = 0; i < kMax; i++)
+      if (gl + i * GL < (int) words) r[i] = src[gl + i * GL];
+#pragma unroll
+    for (int i = 0; i < kMax; i++)
+      if (gl + i * GL < (int) words) ((uint4*) slot)[gl + i * GL] = r[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // (the slot is the group's own: no workgroup barrier)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    base = slot;
+  }
+  uint64_t xr;
+  in_rows<1>(xin, r0, 1, &xr);
+  const int8_t* xq = q + xr * cols;
+  const float* xd = d + xr * nblk;
+  // links i of chain ll: blocks ll + L i < nblk; the first half takes i < ca, the second the rest
+  const uint32_t links = (nblk + L - 1) / L, ca = (links + 1) / 2, i0 = half ? ca : 0, i1 = half ? links : ca;
+  constexpr int kU = L == 16 ? 4 : 8;  // the most links a half takes unrolled (16 lanes: 4096 columns / 512)
+  float sub[kU], xs[kU];
+#pragma unroll
+  for (int k = 0; k < kU; k++) {
+    const uint32_t s = ll + L * (i0 + (uint32_t) k);
+    sub[k] = 0.0f, xs[k] = 0.0f;
+    if (i0 + (uint32_t) k < i1 && s < nblk) {
+      Codes c;
+      codes<T>(base + (s / per) * Block<T>::bytes, (int) (s % per), c, const_grid<T>());
+      int x[8];
+      load_x(xq, (uint64_t) s * 32, x);
+      sub[k] = block_sum<T>(c, x), xs[k] = xd[s];
+    }
+  }
+  // the chain: the first half's links from 0, handed to the second half (lane ll + L), which runs its own
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kU; k++)
+    if (!half && (uint32_t) k < ca && ll + L * (uint32_t) k < nblk) acc = __builtin_fmaf(xs[k], sub[k], acc);
+  acc = L == 16 ? xor_lane(acc, 16) : __shfl_xor(acc, 32, kWave);
+#pragma unroll
+  for (int k = 0; k < kU; k++)
+    if (half && ca + (uint32_t) k < links && ll + L * (ca + (uint32_t) k) < nblk) acc = __builtin_fmaf(xs[k], sub[k], acc);
+  const float v = tree<L>(acc);
+  if (half && ll == 0) y[(uint64_t) r0 * ys + row] = v;
+}
+template <uint32_t T, int L, bool STG>
+__global__ __launch_bounds__(kThreads) void one_kernel(const uint8_t* const* __restrict__ w,
+                                                       const int32_t* __restrict__ cnt, const int32_t* __restrict__ xrow,
+                                                       const int32_t* __restrict__ xin, uint32_t rows, uint32_t cols,
+                                                       const int8_t* __restrict__ q, const float* __restrict__ d,
+                                                       float* __restrict__ y, uint32_t ys) {
+  const uint32_t m = blockIdx.y, row = blockIdx.x * OneShape<L>::rows + threadIdx.x / OneShape<L>::group;
+  if (!cnt[m] || row >= rows) return;  // (no token; or a group past the rows: its tree's partners are its own)
+  const uint8_t* wm = w[m];
+  // (the staged form needs the matrix 16-aligned: known only here, a uniform choice a matrix)
+  if (STG && (uintptr_t) wm % 16 == 0)
+    one_row<T, L, STG>(wm, row, (uint32_t) xrow[m], xin, cols, q, d, y, ys);
+  else
+    one_row<T, L, false>(wm, row, (uint32_t) xrow[m], xin, cols, q, d, y, ys);
+}
+
 // gate and up at once, then the activation (reference kernels/q8.h:214-261)
 template <uint32_t T, int NT, int L>
 __global__ __launch_bounds__(kThreads) void gate_up_kernel(const uint8_t* const* __restrict__ wg,
@@ -183,8 +275,24 @@ bool launch(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
   return hipGetLastError() == hipSuccess;
 }
 
+// one token of q8_group_tok: one_kernel, staged where the type gains by it and the rows allow
+template <uint32_t T, int L>
+bool one_launch(const Args& a, hipStream_t s) {
+  const dim3 grid((a.rows + OneShape<L>::rows - 1) / OneShape<L>::rows, a.n);
+  const uint64_t rb = row_bytes<T>(a.cols);
+  if (one_stages<T>() && rb % 16 == 0 && rb <= kOneStg)
+    one_kernel<T, L, true><<<grid, kThreads, 0, s>>>((const uint8_t* const*) a.wg, a.cnt, a.xrow, a.xin, a.rows,
+                                                      a.cols, a.q, a.d, a.y, a.ys);
+  else
+    one_kernel<T, L, false><<<grid, kThreads, 0, s>>>((const uint8_t* const*) a.wg, a.cnt, a.xrow, a.xin, a.rows,
+                                                       a.cols, a.q, a.d, a.y, a.ys);
+  return hipGetLastError() == hipSuccess;
+}
+
 template <uint32_t T, int NT>
 bool by_lanes(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
+  if (one_serves<T>() && NT == 1 && !fused && a.cols <= 8192)
+    return a.cols >= 4096 ? one_launch<T, 32>(a, s) : one_launch<T, 16>(a, s);
   return a.cols >= 4096 ? launch<T, NT, 32>(a, fused, s, tiles) : launch<T, NT, 16>(a, fused, s, tiles);
 }
 

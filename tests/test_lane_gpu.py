@@ -189,3 +189,29 @@ def test_refusals(g):
     assert not L.q8_group_tok(16, p, p, p, None, 1, 1, 16, 500, p, p, p, 16, None)
     assert not L.q8_gate_up(16, p, p, p, p, None, None, 1, 1, 16, 512, p, p, p, 1.0, p, 8, None)
     assert not L.q8_round(p, 1, 48, 48, p, p, None) and not L.q8_round(p, 1, 64, 32, p, p, None)
+
+
+@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q3_K", "IQ3_XXS"])
+@pytest.mark.parametrize("cols", [2048, 4096])
+def test_group_tok_one_token_unaligned_matrix(g, name, cols):
+    """one token (max_cnt 1: rows a group of 2L lanes, Q4_0 / Q4_K / Q3_K staged through LDS where the matrix is
+    16-aligned): a matrix 8 bytes past a 16-byte boundary (the direct form) and the same matrix aligned give the
+    oracle's bits; two matrices of one launch, one of each"""
+    import torch
+    t = synth.ID[name]
+    rows = 70
+    w = synth.random_blocks(t, rows, cols, 31)
+    n = w.size
+    buf = torch.zeros(n + 64, dtype=torch.uint8, device="cuda")
+    buf[8:8 + n] = torch.from_numpy(np.ascontiguousarray(w).reshape(-1)).cuda()
+    wa = g.dev(w)
+    assert buf[8:8 + n].data_ptr() % 16 == 8 and wa.data_ptr() % 16 == 0
+    x = np.random.default_rng(6).normal(0, 1, (2, cols)).astype(np.float32)
+    q, d = orc.q8_round(x)
+    want = orc.q8_rows(t, w, rows, cols, q, d)
+    y = torch.full((2, rows), float("nan"), device="cuda")
+    print("group_tok one token", name, cols, flush=True)
+    g.call("q8_group_tok", t, g.a(g.table([buf[8:8 + n], wa])), g.a(g.dev(np.array([1, 1], np.int32))),
+           g.a(g.dev(np.array([0, 1], np.int32))), None, 2, 1, rows, cols, g.a(g.dev(q)), g.a(g.dev(d)), g.a(y), rows,
+           None)
+    assert (g.bits(g.host(y)) == g.bits(want)).all()
