@@ -14,8 +14,12 @@ down launch's figures beside it.
 cpu_baseline: the reference's own CPU path (oracle/_ref: src/cpu/q8.c's cpu_q8_rows and kernels/lane.h) on the host's
 cores for the same layer, rows split evenly over the threads as src/cpu/lane.c splits them.
 
---all adds the other BASELINE configs as `extra` lines (Q4_0 / Q4_K / Q3_K GEMV, the DeepSeek IQ1 experts, the mmq
-expert GEMM) - they are reported, not the headline.
+prefill_bs512 (every run): the metric's batch-512 half, config 5's expert GEMMs (int8 TOPS, % of MFMA peak, roofline
+fraction). gemv_bs1 (every run): the metric's GEMV half on configs 1 and 2 at one token (Q4_0 2048 -> 8192, Q4_K and
+Q3_K 2048 -> 6144: the lane's int8 GEMV and the fp32 matvec, HBM GB/s and % of peak).
+
+--all adds the other BASELINE configs as `extra` lines (Q4_K / Q3_K at 8 and 64 tokens, the Qwen layer at 4 and 32,
+the DeepSeek IQ1 experts) - they are reported, not the headline.
 """
 import argparse
 import ctypes
@@ -112,15 +116,16 @@ def graph_us(torch, launch, G, reps=10):
     return ms * 1e3 / (reps * G)
 
 
-def gemv_extras(torch, capi):
+def gemv_extras(torch, capi, bs1_only=False):
     """configs 1 and 2: one matrix (rotated copies, more than 2 GiB) a launch - the fp32 matvec (mv_strided), the lane's
-    int8 matvec (q8_group_tok, x rounded beforehand) and the f16 MFMA matmul (mm_run, x16 beforehand) at 8 / 64"""
+    int8 matvec (q8_group_tok, x rounded beforehand) and the f16 MFMA matmul (mm_run, x16 beforehand) at 8 / 64;
+    bs1_only: one token alone (the metric's GEMV half on its own configs, in every run)"""
     L = capi.lib()
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1)
     out = {}
-    for name, rows, cols, batches in (("Q4_0", 8192, 2048, (1,)), ("Q4_K", 6144, 2048, (1, 8, 64)),
-                                      ("Q3_K", 6144, 2048, (1, 8, 64))):
+    for name, rows, cols, batches in (("Q4_0", 8192, 2048, (1,)), ("Q4_K", 6144, 2048, (1,) if bs1_only else (1, 8, 64)),
+                                      ("Q3_K", 6144, 2048, (1,) if bs1_only else (1, 8, 64))):
         v, b = BLOCK[name]
         wbytes = rows * cols // v * b
         copies = max(2, math.ceil(2.2e9 / wbytes))
@@ -614,6 +619,13 @@ def main():
     torch.cuda.empty_cache()
     prefill = prefill_extras(torch, capi)
     line["prefill_bs512"] = prefill
+    # the metric's GEMV half on configs 1 and 2 (one token, HBM GB/s), in every run
+    log("configs 1, 2 at one token")
+    torch.cuda.empty_cache()
+    gemv = gemv_extras(torch, capi, bs1_only=True)
+    for v in gemv.values():
+        v["pct_hbm_peak"] = round(100 * v["GB/s"] / HBM_PEAK_GBS, 2)
+    line["gemv_bs1"] = gemv
     if args.all:
         torch.cuda.empty_cache()
         extra = {}
@@ -626,6 +638,7 @@ def main():
             torch.cuda.empty_cache()
         if "12" in only:
             log("configs 1, 2")
+            torch.cuda.empty_cache()
             extra.update(gemv_extras(torch, capi))
         if "4" in only:
             log("config 4")
