@@ -7,6 +7,8 @@ pinned oracle:
   of the matrix), the lane at 1 and 8 tokens (every row), mm_run at 8 and 64 tokens within the reference's f16 bound;
 - config 3: the Qwen-style layer at its full expert count (512 experts, hidden 2048, expert ff 512, top-10, IQ3_XXS)
   at batches 1 and 32;
+- config 4: the DeepSeek-style layer at its full expert count (256 routed + the shared one, hidden 7168, expert ff
+  2048, top-9) in IQ1_S and IQ1_M at batches 1 and 4;
 - config 5: the benchmark's own routing (512 tokens top-8 of 256 experts, Zipf 1.1, seed 11): mmq_group over Q4_K
   2048 -> 7168 and osmos_lane_group over IQ2_XXS 7168 -> 2048, every expert launched; the busiest expert (all of its
   tokens) and two small ones checked on 64-row subsets, and tokens of the busiest expert run alone for batch
@@ -141,6 +143,53 @@ def test_config3_qwen_layer_512_experts(g, n_tok):
                   g.dev(Dn).reshape(n_exp, -1))
     out = torch.full((n_tok, dim), float("nan"), device="cuda")
     print("config 3 layer, 512 experts", n_tok, flush=True)
+    L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
+    assert (g.bits(g.host(out)) == g.bits(want)).all()
+
+
+def _device_blocks(g, name, n, seed):
+    """n blocks of `name` as random bytes made on the device, each scale an f16 in [2^-4, 2^-3) (synth's fill):
+    returns uint8 [n, block bytes]"""
+    import torch
+    _, _, b = synth.TYPES[synth.ID[name]]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    blk = torch.randint(0, 256, (n, b), dtype=torch.uint8, device="cuda", generator=gen)
+    h = 0x2C00 | torch.randint(0, 1024, (n,), dtype=torch.int32, device="cuda", generator=gen)
+    if name == "IQ1_M":  # the f16's nibble k in the top nibble of scale word k
+        for k in range(4):
+            at = 48 + 2 * k + 1
+            blk[:, at] = (blk[:, at] & 0x0F) | (((h >> (4 * k)) & 0x0F) << 4).to(torch.uint8)
+    else:
+        blk[:, 0] = (h & 0xFF).to(torch.uint8)
+        blk[:, 1] = ((h >> 8) & 0xFF).to(torch.uint8)
+    return blk
+
+
+@pytest.mark.parametrize("name", ["IQ1_S", "IQ1_M"])
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_config4_deepseek_layer_257_experts(g, name, n_tok):
+    """the DeepSeek-style layer at its full expert count: 256 routed experts plus the shared one as a ninth pick
+    (257 matrices of each kind, hidden 7168, expert ff 2048), IQ1_S and IQ1_M, batches 1 and 4 (the draft/verify
+    batch): the oracle's bits. (weights made on the device; the routed experts' copied back for the oracle)"""
+    import torch
+    from libosmos_amd.layer import LaneLayer
+    from tests.test_moe_gpu import _lane_layer_oracle
+    t = synth.ID[name]
+    n_exp, k, dim, ff = 257, 9, 7168, 2048
+    per = dim // 256 * ff  # blocks a matrix (gate / up: ff rows of dim; down: dim rows of ff)
+    mats = [_device_blocks(g, name, n_exp * per, 400 + 10 * n_tok + i).reshape(n_exp, -1) for i in range(3)]
+    rng = np.random.default_rng(90 + n_tok)
+    x = rng.normal(0, 1, (n_tok, dim)).astype(np.float32)
+    ids = np.stack([np.concatenate([rng.choice(n_exp - 1, k - 1, replace=False), [n_exp - 1]]) for _ in range(n_tok)])
+    ids = ids.astype(np.int32)
+    wts = rng.uniform(0.01, 0.3, (n_tok, k)).astype(np.float32)
+    used = sorted(set(ids.reshape(-1).tolist()))
+    host = [{e: g.host(m[e]).reshape(dim if i == 2 else ff, -1) for e in used} for i, m in enumerate(mats)]
+    want = _lane_layer_oracle(t, x, ids, wts, host[0], host[1], host[2], dim, ff, math.inf)
+    L = LaneLayer(t, t, dim, ff, n_exp, k, *mats)
+    out = torch.full((n_tok, dim), float("nan"), device="cuda")
+    print("config 4 layer, 257 experts", name, n_tok, flush=True)
     L.forward(g.dev(x), g.dev(ids), g.dev(wts), torch.zeros((n_tok, dim), device="cuda"), out)
     assert (g.bits(g.host(out)) == g.bits(want)).all()
 
