@@ -184,7 +184,7 @@ constexpr int kGroup = 8;
 // wave holds L / W chains x G groups x 2 accumulators, and each decoded block serves G groups. measured on config 5's
 // routing (512 tokens, 250 experts, the busiest 441) at 2048 x 7168 (us): IQ2_XXS G/W 2/4 1609, 1/8 1320, 2/8 1355,
 // 4/8 1582, 2/16 1356; IQ3_XXS 2/4 3159, 2/8 1742, 4/8 1664, 2/16 1413, 1/16 1485; IQ1_M 2/4 2068, 2/8 1426, 2/16
-// 1472; at 7168 x 2048 (16 lanes) IQ2_XXS 2/4 1352, 4/4 1602, 8/4 2598, 2/8 1432. (IQ2_XXS at 1/8: 1322 against 1355) (IQ3_XXS's 16 KB signed codebook
+// 1472; at 7168 x 2048 (16 lanes) IQ2_XXS 2/4 1352, 4/4 1602, 8/4 2598, 2/8 1432. (IQ3_XXS's 16 KB signed codebook
 // and 44 KB slab leave room for two workgroups a CU: it wants the most waves)
 struct Shape {
   int g, w;
