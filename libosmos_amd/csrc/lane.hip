@@ -80,6 +80,92 @@ template <int L> struct OneShape {
 template <uint32_t T> constexpr bool one_serves() { return T == kQ4_K || T == kQ3_K; }
 template <uint32_t T> constexpr bool one_stages() { return T == kQ4_K; }
 
+// a lane's run of block bytes held in registers (wide_kernel's 36 words), read by the decoders (codes<T> takes it as its block
+// pointer) at byte offsets that are compile-time constants: each read folds to a register and a shift
+struct RegBytes {
+  const uint32_t* w;
+  int off;
+  __device__ RegBytes operator+(int o) const { return {w, off + o}; }
+  __device__ uint32_t operator[](int i) const { return (w[(off + i) >> 2] >> (8 * ((off + i) & 3))) & 0xFFu; }
+};
+__device__ inline uint32_t ld16(RegBytes p) {
+  if ((p.off & 3) == 3) return p[0] | p[1] << 8;
+  return (p.w[p.off >> 2] >> (8 * (p.off & 3))) & 0xFFFFu;
+}
+__device__ inline uint32_t ld16s(RegBytes p) { return ld16(p); }
+
+// one token of a type whose 8 contract blocks are 144 bytes - nine 16-byte words (Q4_0: 8 blocks of 18 bytes; Q4_K:
+// one super-block): lane p of a row's R lanes loads blocks 8 p .. 8 p + 7 with 9 wide loads and sums each
+// (block_sum, x from LDS) into the row's LDS line; then each lane runs the contract's chains ll = p + R c (C = L / R of
+// them: blocks ll, ll + L, ... in order, acc = fmaf(x's scale, sum, acc)), the tree's levels L/2 .. R in its own
+// registers and R/2 .. 1 across the row's lanes - the contract's steps in its order, group_tok_kernel's bits.
+// (a matrix that is not 16-aligned: the same words from two-byte loads)
+template <uint32_t T>
+constexpr bool wide_serves() {
+  return T == kQ4_0 || T == kQ4_K;
+}
+template <uint32_t T, int L, int R, int NTH>
+__global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
+                                                   const int32_t* __restrict__ xrow, const int32_t* __restrict__ xin,
+                                                   uint32_t rows, const int8_t* __restrict__ q,
+                                                   const float* __restrict__ d, float* __restrict__ y, uint32_t ys) {
+  constexpr int RW = NTH / R, nblk = 8 * R, C = L / R, cols = 32 * nblk;
+  constexpr uint32_t rb = 144 * R;
+  static_assert(C >= 1 && R <= 32, "a row's lanes within a 32-lane group, chains whole");
+  __shared__ __attribute__((aligned(16))) int8_t xq[cols];
+  __shared__ float xd[nblk];
+  __shared__ __attribute__((aligned(16))) float subs[RW][nblk + 4];  // (+4: the rows' lines on different banks)
+  const uint32_t m = blockIdx.y;
+  if (!cnt[m]) return;  // (an entry past a device-built table's live ones: nothing read or written)
+  const int t = threadIdx.x, rl = t / R, p = t % R;
+  const uint32_t row = blockIdx.x * RW + rl;
+  const uint8_t* src = w[m] + (uint64_t) (row < rows ? row : 0) * rb + 144 * p;
+  uint32_t W[36];
+  if (((uintptr_t) w[m] & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      const uint4 v = ((const uint4*) src)[i];
+      W[4 * i] = v.x, W[4 * i + 1] = v.y, W[4 * i + 2] = v.z, W[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 36; i++) W[i] = osm::ld16(src + 4 * i) | osm::ld16(src + 4 * i + 2) << 16;
+  }
+  uint64_t xr;
+  in_rows<1>(xin, (uint32_t) xrow[m], 1, &xr);
+  for (int i = t; i < cols / 16; i += NTH) ((int4*) xq)[i] = ((const int4*) (q + xr * cols))[i];
+  for (int i = t; i < nblk; i += NTH) xd[i] = d[xr * nblk + i];
+  __syncthreads();
+  float sub[8];
+#pragma unroll
+  for (int b = 0; b < 8; b++) {
+    Codes c;
+    if constexpr (T == kQ4_0) codes<T>(RegBytes{W, 18 * b}, 0, c, nullptr);
+    else codes<T>(RegBytes{W, 0}, b, c, nullptr);
+    int x[8];
+    load_x(xq, (uint64_t) (8 * p + b) * 32, x);
+    sub[b] = block_sum<T>(c, x);
+  }
+  ((float4*) &subs[rl][8 * p])[0] = make_float4(sub[0], sub[1], sub[2], sub[3]);
+  ((float4*) &subs[rl][8 * p])[1] = make_float4(sub[4], sub[5], sub[6], sub[7]);
+  __syncthreads();
+  float acc[C];
+#pragma unroll
+  for (int c = 0; c < C; c++) {
+    acc[c] = 0.0f;
+#pragma unroll
+    for (int s = p + R * c; s < nblk; s += L) acc[c] = __builtin_fmaf(xd[s], subs[rl][s], acc[c]);
+  }
+#pragma unroll
+  for (int o = C / 2; o > 0; o >>= 1)
+#pragma unroll
+    for (int c = 0; c < o; c++) acc[c] = __fadd_rn(acc[c], acc[c + o]);
+  float v = acc[0];
+#pragma unroll
+  for (int o = R / 2; o > 0; o >>= 1) v = __fadd_rn(v, xor_lane(v, o));
+  if (p == 0 && row < rows) y[(uint64_t) (uint32_t) xrow[m] * ys + row] = v;
+}
+
 template <uint32_t T, int L, bool STG>
 __device__ __forceinline__ void one_row(const uint8_t* wm, uint32_t row, uint32_t r0, const int32_t* __restrict__ xin,
                                         uint32_t cols, const int8_t* __restrict__ q, const float* __restrict__ d,
@@ -289,8 +375,38 @@ bool one_launch(const Args& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess;
 }
 
+// one token on wide_kernel (R: a row's lanes, cols / 256); false: not taken
+template <uint32_t T, int L, int R>
+bool wide_launch_r(const Args& a, hipStream_t s) {
+  // (a wave a workgroup: measured at one token on config 1's Q4_0 2048 -> 8192 / config 2's Q4_K 2048 -> 6144, us:
+  // 64 threads 5.63 / 5.08, 128 6.12 / 6.05, 256 5.55 / 6.04; two lanes a chunk, 4 blocks each, no faster)
+  constexpr int kN = 64, RW = kN / R;
+  const dim3 grid((a.rows + RW - 1) / RW, a.n);
+  wide_kernel<T, L, R, kN><<<grid, kN, 0, s>>>((const uint8_t* const*) a.wg, a.cnt, a.xrow, a.xin, a.rows, a.q, a.d,
+                                               a.y, a.ys);
+  return hipGetLastError() == hipSuccess;
+}
+template <uint32_t T>
+bool wide_launch(const Args& a, hipStream_t s, bool* taken) {
+  *taken = true;
+  switch (a.cols) {
+    case 1024: return wide_launch_r<T, 16, 4>(a, s);
+    case 2048: return wide_launch_r<T, 16, 8>(a, s);
+    case 4096: return wide_launch_r<T, 32, 16>(a, s);
+    case 8192: return wide_launch_r<T, 32, 32>(a, s);
+    default: *taken = false; return false;
+  }
+}
+
 template <uint32_t T, int NT>
 bool by_lanes(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
+  if constexpr (wide_serves<T>() && NT == 1) {
+    bool taken = false;
+    if (!fused) {
+      const bool ok = wide_launch<T>(a, s, &taken);
+      if (taken) return ok;
+    }
+  }
   if (one_serves<T>() && NT == 1 && !fused && a.cols <= 8192)
     return a.cols >= 4096 ? one_launch<T, 32>(a, s) : one_launch<T, 16>(a, s);
   return a.cols >= 4096 ? launch<T, NT, 32>(a, fused, s, tiles) : launch<T, NT, 16>(a, fused, s, tiles);

@@ -215,3 +215,29 @@ def test_group_tok_one_token_unaligned_matrix(g, name, cols):
            g.a(g.dev(np.array([0, 1], np.int32))), None, 2, 1, rows, cols, g.a(g.dev(q)), g.a(g.dev(d)), g.a(y), rows,
            None)
     assert (g.bits(g.host(y)) == g.bits(want)).all()
+
+
+@pytest.mark.parametrize("name", ["Q4_0", "Q4_K"])
+@pytest.mark.parametrize("cols", [1024, 2048, 4096, 8192])
+def test_group_tok_one_token_wide(g, name, cols):
+    """one token of Q4_0 / Q4_K at the widths whose rows split into 144-byte runs of 8 blocks a lane (1024 - 8192
+    columns, 16 and 32 logical lanes): three matrices in one launch - ragged rows, tokens picked through xin, one
+    matrix with no token (nothing written) - each the oracle's bits"""
+    import torch
+    t = synth.ID[name]
+    rows = 37
+    ws = [synth.random_blocks(t, rows, cols, 50 + m) for m in range(3)]
+    x = np.random.default_rng(cols).normal(0, 1, (4, cols)).astype(np.float32)
+    q, d = orc.q8_round(x)
+    xin = np.array([3, 0, 2], np.int32)  # matrix m's token: input row xin[xrow[m]]
+    y = torch.full((3, rows), float("nan"), device="cuda")
+    print("group_tok one token wide", name, cols, flush=True)
+    g.call("q8_group_tok", t, g.a(g.table([g.dev(w) for w in ws])), g.a(g.dev(np.array([1, 0, 1], np.int32))),
+           g.a(g.dev(np.array([0, 1, 2], np.int32))), g.a(g.dev(xin)), 3, 1, rows, cols, g.a(g.dev(q)), g.a(g.dev(d)),
+           g.a(y), rows, None)
+    got = g.host(y)
+    for m in (0, 2):
+        r = xin[m]
+        want = orc.q8_rows(t, ws[m], rows, cols, q[r:r + 1], d[r:r + 1])
+        assert (g.bits(got[m]) == g.bits(want[0])).all(), (name, cols, m)
+    assert np.isnan(got[1]).all()
