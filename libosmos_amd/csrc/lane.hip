@@ -8,6 +8,8 @@
 //
 // CDNA4 mapping: a wave64 holds 64 / L rows (4 at 16 lanes, 2 at 32), logical lane ll = lane % L of row lane / L -
 // the tree's partners (ll ^ o, o < L) stay inside the row's aligned group of lanes. a workgroup is 4 waves.
+#include <type_traits>
+
 #include "lanedec.h"
 
 extern "C" {
@@ -77,7 +79,7 @@ template <int L> struct OneShape {
 // the types it serves and those it stages: measured on config 2's 2048 -> 6144 and config 1's 2048 -> 8192 at one
 // token (us, group_tok_kernel / one_kernel direct / one_kernel staged): Q4_K 8.49 / - / 7.87, Q3_K 7.49 / 6.68 / 8.25,
 // Q4_0 5.97 / 6.36 / 8.97 (Q4_0 stays with group_tok_kernel)
-template <uint32_t T> constexpr bool one_serves() { return T == kQ4_K || T == kQ3_K; }
+template <uint32_t T> constexpr bool one_serves() { return T == kQ4_K || T == kQ3_K; }  // (widths wide_kernel does not take)
 template <uint32_t T> constexpr bool one_stages() { return T == kQ4_K; }
 
 // a lane's run of block bytes held in registers (wide_kernel's 36 words), read by the decoders (codes<T> takes it as its block
@@ -100,9 +102,24 @@ __device__ inline uint32_t ld16s(RegBytes p) { return ld16(p); }
 // them: blocks ll, ll + L, ... in order, acc = fmaf(x's scale, sum, acc)), the tree's levels L/2 .. R in its own
 // registers and R/2 .. 1 across the row's lanes - the contract's steps in its order, group_tok_kernel's bits.
 // (a matrix that is not 16-aligned: the same words from two-byte loads)
+template <int B, typename F>
+__device__ __forceinline__ void each8(F&& f) {
+  if constexpr (B < 8) {
+    f(std::integral_constant<int, B>());
+    each8<B + 1>(f);
+  }
+}
+
+// Q3_K's 8 contract blocks are one 110-byte super-block, 2-aligned: a lane loads the 8 16-byte words that cover it (a
+// buffer descriptor from the matrix's 16-byte-aligned start: words past the end read as zeros) and shifts them in
+// registers to the chunk's first byte (a two-step dword select, then a byte align by 0 or 2)
 template <uint32_t T>
 constexpr bool wide_serves() {
-  return T == kQ4_0 || T == kQ4_K;
+  return T == kQ4_0 || T == kQ4_K || T == kQ3_K;
+}
+template <uint32_t T>
+constexpr uint32_t wide_chunk() {
+  return T == kQ3_K ? 110 : 144;
 }
 template <uint32_t T, int L, int R, int NTH>
 __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
@@ -110,7 +127,7 @@ __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restr
                                                    uint32_t rows, const int8_t* __restrict__ q,
                                                    const float* __restrict__ d, float* __restrict__ y, uint32_t ys) {
   constexpr int RW = NTH / R, nblk = 8 * R, C = L / R, cols = 32 * nblk;
-  constexpr uint32_t rb = 144 * R;
+  constexpr uint32_t CB = wide_chunk<T>(), rb = CB * R;
   static_assert(C >= 1 && R <= 32, "a row's lanes within a 32-lane group, chains whole");
   __shared__ __attribute__((aligned(16))) int8_t xq[cols];
   __shared__ float xd[nblk];
@@ -119,9 +136,30 @@ __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restr
   if (!cnt[m]) return;  // (an entry past a device-built table's live ones: nothing read or written)
   const int t = threadIdx.x, rl = t / R, p = t % R;
   const uint32_t row = blockIdx.x * RW + rl;
-  const uint8_t* src = w[m] + (uint64_t) (row < rows ? row : 0) * rb + 144 * p;
+  const uint8_t* src = w[m] + (uint64_t) (row < rows ? row : 0) * rb + CB * p;
   uint32_t W[36];
-  if (((uintptr_t) w[m] & 15) == 0) {
+  if constexpr (CB % 16) {
+    const uintptr_t a0 = (uintptr_t) w[m] & ~(uintptr_t) 15, at = (uintptr_t) src;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void*) a0, (short) 0, (int) ((uintptr_t) w[m] - a0 + (uint64_t) rows * rb), 0x00020000);
+    const uint32_t o = (uint32_t) ((at & ~(uintptr_t) 15) - a0), sh = (uint32_t) (at & 15);
+    uint32_t V[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+      const u4 v = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, o + 16 * i, 0, 0));
+      V[4 * i] = v.x, V[4 * i + 1] = v.y, V[4 * i + 2] = v.z, V[4 * i + 3] = v.w;
+    }
+    // (the selects as byte permutes of a dword pair: a conditional the compiler would turn into a load at a run-time
+    // index, which puts the array in scratch memory)
+    const uint32_t p1 = sh & 4 ? 0x07060504u : 0x03020100u, p2 = sh & 8 ? 0x07060504u : 0x03020100u;
+#pragma unroll
+    for (int i = 0; i < 31; i++) V[i] = __builtin_amdgcn_perm(V[i + 1], V[i], p1);
+#pragma unroll
+    for (int i = 0; i < 29; i++) V[i] = __builtin_amdgcn_perm(V[i + 2], V[i], p2);
+#pragma unroll
+    for (int i = 0; i < 28; i++) W[i] = __builtin_amdgcn_alignbyte(V[i + 1], V[i], sh & 3);
+  } else if (((uintptr_t) w[m] & 15) == 0) {
 #pragma unroll
     for (int i = 0; i < 9; i++) {
       const uint4 v = ((const uint4*) src)[i];
@@ -137,15 +175,15 @@ __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restr
   for (int i = t; i < nblk; i += NTH) xd[i] = d[xr * nblk + i];
   __syncthreads();
   float sub[8];
-#pragma unroll
-  for (int b = 0; b < 8; b++) {
+  each8<0>([&](auto bc) __attribute__((always_inline)) {  // (unrolled by construction: every offset a constant)
+    constexpr int b = decltype(bc)::value;
     Codes c;
     if constexpr (T == kQ4_0) codes<T>(RegBytes{W, 18 * b}, 0, c, nullptr);
-    else codes<T>(RegBytes{W, 0}, b, c, nullptr);
+    else codes<T>(RegBytes{W, 0}, b, c, nullptr);  // (Q4_K, Q3_K: block b of the super-block)
     int x[8];
     load_x(xq, (uint64_t) (8 * p + b) * 32, x);
     sub[b] = block_sum<T>(c, x);
-  }
+  });
   ((float4*) &subs[rl][8 * p])[0] = make_float4(sub[0], sub[1], sub[2], sub[3]);
   ((float4*) &subs[rl][8 * p])[1] = make_float4(sub[4], sub[5], sub[6], sub[7]);
   __syncthreads();

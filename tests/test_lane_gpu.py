@@ -217,12 +217,13 @@ def test_group_tok_one_token_unaligned_matrix(g, name, cols):
     assert (g.bits(g.host(y)) == g.bits(want)).all()
 
 
-@pytest.mark.parametrize("name", ["Q4_0", "Q4_K"])
+@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q3_K"])
 @pytest.mark.parametrize("cols", [1024, 2048, 4096, 8192])
 def test_group_tok_one_token_wide(g, name, cols):
-    """one token of Q4_0 / Q4_K at the widths whose rows split into 144-byte runs of 8 blocks a lane (1024 - 8192
-    columns, 16 and 32 logical lanes): three matrices in one launch - ragged rows, tokens picked through xin, one
-    matrix with no token (nothing written) - each the oracle's bits"""
+    """one token of Q4_0 / Q4_K / Q3_K at the widths whose rows split into runs of 8 contract blocks a lane (144 bytes;
+    Q3_K's 110, shifted into place in registers) over 1024 - 8192 columns, 16 and 32 logical lanes: three matrices in
+    one launch - ragged rows, tokens picked through xin, one matrix with no token (nothing written) - each the
+    oracle's bits"""
     import torch
     t = synth.ID[name]
     rows = 37
