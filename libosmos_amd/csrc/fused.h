@@ -576,23 +576,50 @@ struct G1Lds {
   static constexpr uint32_t total = w + align16(2 * kG1Rows * (uint32_t) row_bytes<T>(D));
 };
 
-// S: staging slots a matrix (the fewest that hold its tile rows); L: the contract's lanes a row (16 or 32)
-template <uint32_t T, int S, int L, bool P = false>
-__global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
+// q8_gate_up's operands for gu1_item (TAB): matrix m's gate and up rows from the pointer tables, its token's input row
+// xin[xrow[m]] (or xrow[m]) of the rounded q / d, its scale scale[win[xrow[m]]] (or scale[xrow[m]]), its h row
+// xrow[m] (hs floats apart); a matrix with no token is skipped
+struct G1Tab {
+  const uint8_t* const* wg;
+  const uint8_t* const* wu;
+  const int32_t *cnt, *xrow, *xin, *win;
+  const int8_t* q;
+  const float *d, *scale;
+  float* h;
+  uint32_t hs;
+};
+
+// one gate/up tile of one token: the layer's (pick m's expert ids[m], its rows at gate + id gate_bytes, router weight
+// w[m], h row m) or, TAB, q8_gate_up's matrix m (tb). S: staging slots a matrix (the fewest that hold its tile rows);
+// L: the contract's lanes a row (16 or 32)
+template <uint32_t T, int S, int L, bool P = false, bool TAB = false>
+__device__ __forceinline__ void gu1_item(const GuArgs& a, const G1Tab& tb, uint32_t m, uint32_t tile, uint8_t* smem) {
   using LD = G1Lds<T, L>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[LD::total];
   constexpr int kThreads = kG1Threads;
   constexpr uint32_t per = Block<T>::values / 32, bb = Block<T>::bytes;
   constexpr int R = (int) (G1Max<L>::dim / 32 / (kThreads / 4));  // x's rounding rounds (4 lanes a block)
-  const uint32_t m = blockIdx.y, r0 = blockIdx.x * kG1Rows;
+  static_assert(!TAB || P, "q8_gate_up's x is rounded already");
+  const uint32_t r0 = tile * kG1Rows;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.dim), nblk = a.dim / 32;
   const uint32_t per_seg = kG1Rows * rb / 16;  // a matrix's words
   // the lane's word of each slot (past the matrix's end: its last word again, loaded and not stored)
   uint32_t idx[S];
 #pragma unroll
   for (uint32_t u = 0; u < (uint32_t) S; u++) idx[u] = min(u * kThreads + threadIdx.x, per_seg - 1);
-  const uint32_t e = (uint32_t) a.ids[m];  // (an expert id: not negative; unsigned, so no sign extension to wait for)
-  const float wm = a.w[m];
+  uint32_t e = 0, rout = 0;
+  float wm;
+  const int8_t* xq = a.xq;
+  const float* xdp = a.xd;
+  if constexpr (TAB) {
+    if (!tb.cnt[m]) return;  // (the whole workgroup)
+    rout = (uint32_t) tb.xrow[m];
+    const uint32_t rin = tb.xin ? (uint32_t) tb.xin[rout] : rout;
+    wm = tb.scale[tb.win ? (uint32_t) tb.win[rout] : rout];
+    xq = tb.q + (uint64_t) rin * a.dim, xdp = tb.d + (uint64_t) rin * nblk;
+  } else {
+    e = (uint32_t) a.ids[m];  // (an expert id: not negative; unsigned, so no sign extension to wait for)
+    wm = a.w[m];
+  }
   GridStage<T, kThreads> gs;
   grid_load(gs);
   // the one token's row: rounded here, or (P) its codes and scales already rounded, copied
@@ -603,8 +630,8 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   if constexpr (P) {
     const uint32_t nw = a.dim / 16;
 #pragma unroll
-    for (int r = 0; r < RQ; r++) xw[r] = ((const u32x4*) a.xq)[min(r * kThreads + threadIdx.x, nw - 1)];
-    xs = a.xd[min((uint32_t) threadIdx.x, nblk - 1)];  // (nblk <= 256 = kThreads)
+    for (int r = 0; r < RQ; r++) xw[r] = ((const u32x4*) xq)[min(r * kThreads + threadIdx.x, nw - 1)];
+    xs = xdp[min((uint32_t) threadIdx.x, nblk - 1)];  // (nblk <= 256 = kThreads)
   } else {
     auto xval = [=](uint32_t blk, uint32_t c) __attribute__((always_inline)) { return a.x + blk * 32 + c; };
 #pragma unroll
@@ -613,11 +640,29 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   }
   // (a scheduling barrier: the codebook and x loads issue before the id is waited for)
   __builtin_amdgcn_sched_barrier(0);
-  const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
-  const u32x4* usrc = (const u32x4*) (a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb);
   u32x4 wv[2 * S];
+  if constexpr (TAB) {
+    const uint8_t* gb = tb.wg[m] + (uint64_t) r0 * rb;
+    const uint8_t* ub = tb.wu[m] + (uint64_t) r0 * rb;
+    if ((((uintptr_t) gb | (uintptr_t) ub) & 15) == 0) {
 #pragma unroll
-  for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = gsrc[idx[u]], wv[S + u] = usrc[idx[u]];
+      for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = ((const u32x4*) gb)[idx[u]], wv[S + u] = ((const u32x4*) ub)[idx[u]];
+    } else {  // (a matrix that is not 16-aligned: the same words from two-byte loads)
+      auto w16 = [](const uint8_t* p) __attribute__((always_inline)) {
+        u32x4 v;
+        v.x = osm::ld16(p) | osm::ld16(p + 2) << 16, v.y = osm::ld16(p + 4) | osm::ld16(p + 6) << 16;
+        v.z = osm::ld16(p + 8) | osm::ld16(p + 10) << 16, v.w = osm::ld16(p + 12) | osm::ld16(p + 14) << 16;
+        return v;
+      };
+#pragma unroll
+      for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = w16(gb + 16 * idx[u]), wv[S + u] = w16(ub + 16 * idx[u]);
+    }
+  } else {
+    const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
+    const u32x4* usrc = (const u32x4*) (a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb);
+#pragma unroll
+    for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = gsrc[idx[u]], wv[S + u] = usrc[idx[u]];
+  }
   int8_t* q = (int8_t*) (smem + LD::q);
   float* d = (float*) (smem + LD::d);
   grid_store(gs, smem + LD::grid);
@@ -687,7 +732,24 @@ __global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
   }
   const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
   const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  if (lane == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);
+  if constexpr (TAB) {
+    if (lane == 0) tb.h[(uint64_t) rout * tb.hs + r0 + row] = lane_swiglu(g, u, a.lim, wm);
+  } else {
+    if (lane == 0) a.h[(uint64_t) m * a.ff + r0 + row] = lane_swiglu(g, u, a.lim, wm);
+  }
+}
+
+template <uint32_t T, int S, int L, bool P = false>
+__global__ __launch_bounds__(kG1Threads) void gu1_kernel(GuArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[G1Lds<T, L>::total];
+  gu1_item<T, S, L, P>(a, G1Tab{}, blockIdx.y, blockIdx.x, smem);
+}
+
+// q8_gate_up at one token a matrix on gu1_kernel's tile: workgroup (tile of 4 rows, matrix m)
+template <uint32_t T, int S, int L>
+__global__ __launch_bounds__(kG1Threads) void gu1_tab_kernel(GuArgs a, G1Tab tb) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[G1Lds<T, L>::total];
+  gu1_item<T, S, L, true, true>(a, tb, blockIdx.y, blockIdx.x, smem);
 }
 
 // gub_kernel: gate/up for a batch (n_tok >= 2), gu1_kernel's tile and lane layout with several tokens a pass.

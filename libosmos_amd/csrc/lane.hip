@@ -10,7 +10,7 @@
 // the tree's partners (ll ^ o, o < L) stay inside the row's aligned group of lanes. a workgroup is 4 waves.
 #include <type_traits>
 
-#include "lanedec.h"
+#include "fused.h"
 
 extern "C" {
 #include "../../include/osmos/gpu/mv.h"
@@ -436,8 +436,41 @@ bool wide_launch(const Args& a, hipStream_t s, bool* taken) {
   }
 }
 
+// q8_gate_up at one token a matrix on the fused layer's gate/up tile (fused::gu1_tab_kernel): where its widths, tile
+// rows and staging fit (false in *taken: not taken)
+template <uint32_t T, int L>
+bool tab_launch_l(const Args& a, hipStream_t s, uint32_t words) {
+  fused::GuArgs ga{};
+  ga.dim = a.cols, ga.ff = a.rows, ga.lim = a.lim;
+  const fused::G1Tab tb = {(const uint8_t* const*) a.wg, (const uint8_t* const*) a.wu, a.cnt, a.xrow, a.xin, a.win,
+                           a.q, a.d, a.scale, a.y, a.ys};
+  const dim3 grid(a.rows / fused::kG1Rows, a.n);
+  constexpr int kT = fused::kG1Threads;
+  if (words <= (uint32_t) kT) fused::gu1_tab_kernel<T, 1, L><<<grid, kT, 0, s>>>(ga, tb);
+  else if (words <= 2u * kT) fused::gu1_tab_kernel<T, 2, L><<<grid, kT, 0, s>>>(ga, tb);
+  else fused::gu1_tab_kernel<T, fused::kG1Slots, L><<<grid, kT, 0, s>>>(ga, tb);
+  return hipGetLastError() == hipSuccess;
+}
+template <uint32_t T>
+bool tab_launch(const Args& a, hipStream_t s, bool* taken) {
+  const uint32_t rb = (uint32_t) row_bytes<T>(a.cols), words = fused::kG1Rows * rb / 16;
+  *taken = a.rows % fused::kG1Rows == 0 && (fused::kG1Rows * rb) % 16 == 0 && words <= fused::kG1Slots * fused::kG1Threads;
+  if (*taken && a.cols % 512 == 0 && a.cols <= fused::G1Max<16>::dim) return tab_launch_l<T, 16>(a, s, words);
+  if (*taken && a.cols % 1024 == 0 && a.cols >= 4096 && a.cols <= fused::G1Max<32>::dim)
+    return tab_launch_l<T, 32>(a, s, words);
+  *taken = false;
+  return false;
+}
+
 template <uint32_t T, int NT>
 bool by_lanes(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
+  if constexpr (NT == 1) {
+    if (fused) {
+      bool taken = false;
+      const bool ok = tab_launch<T>(a, s, &taken);
+      if (taken) return ok;
+    }
+  }
   if constexpr (wide_serves<T>() && NT == 1) {
     bool taken = false;
     if (!fused) {
@@ -445,8 +478,8 @@ bool by_lanes(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
       if (taken) return ok;
     }
   }
-  if (one_serves<T>() && NT == 1 && !fused && a.cols <= 8192)
-    return a.cols >= 4096 ? one_launch<T, 32>(a, s) : one_launch<T, 16>(a, s);
+  if constexpr (one_serves<T>() && NT == 1)
+    if (!fused && a.cols <= 8192) return a.cols >= 4096 ? one_launch<T, 32>(a, s) : one_launch<T, 16>(a, s);
   return a.cols >= 4096 ? launch<T, NT, 32>(a, fused, s, tiles) : launch<T, NT, 16>(a, fused, s, tiles);
 }
 

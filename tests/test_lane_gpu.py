@@ -242,3 +242,54 @@ def test_group_tok_one_token_wide(g, name, cols):
         want = orc.q8_rows(t, ws[m], rows, cols, q[r:r + 1], d[r:r + 1])
         assert (g.bits(got[m]) == g.bits(want[0])).all(), (name, cols, m)
     assert np.isnan(got[1]).all()
+
+
+@pytest.mark.parametrize("name", ALL_TYPES)
+@pytest.mark.parametrize("cols", [2048, 4096])
+def test_gate_up_one_token(g, name, cols):
+    """q8_gate_up at one token a matrix (the reference engine's decode step; on the fused layer's gate/up tile where
+    rows come in whole tiles of 4): four matrices - one with no token (nothing written), one 8 bytes past a 16-byte
+    boundary - tokens picked through xin, scales through win, a finite clamp: the oracle's bits; and 70 rows (not whole
+    tiles) the same"""
+    import torch
+    t = synth.ID[name]
+    if cols % synth.TYPES[t][1]:
+        pytest.skip("the type's blocks do not divide the width")
+    L = orc.orc()
+    rng = np.random.default_rng(cols + t)
+    x = rng.normal(0, 1, (5, cols)).astype(np.float32)
+    q, d = orc.q8_round(x)
+    scale = rng.uniform(0.05, 1, 8).astype(np.float32)
+    for rows in (96, 70):
+        wg = [synth.random_blocks(t, rows, cols, 500 + m) for m in range(4)]
+        wu = [synth.random_blocks(t, rows, cols, 600 + m) for m in range(4)]
+        counts = np.array([1, 0, 1, 1], np.int32)
+        xrow = np.array([3, 0, 1, 2], np.int32)  # matrix m's h row
+        xin = np.array([4, 0, 2, 1], np.int32)   # h row r's input row
+        win = np.array([6, 1, 3, 0], np.int32)   # h row r's scale
+        lim = 1.5
+        # matrix 2's gate and up 8 bytes past a 16-byte boundary
+        n = wg[2].size
+        bufs = []
+        for w in (wg[2], wu[2]):
+            b = torch.zeros(n + 64, dtype=torch.uint8, device="cuda")
+            b[8:8 + n] = torch.from_numpy(np.ascontiguousarray(w).reshape(-1)).cuda()
+            bufs.append(b)
+        tg = [g.dev(w) for w in wg]
+        tu = [g.dev(w) for w in wu]
+        tg[2], tu[2] = bufs[0][8:8 + n], bufs[1][8:8 + n]
+        h = torch.full((4, rows), float("nan"), device="cuda")
+        print("gate_up one token", name, cols, rows, flush=True)
+        g.call("q8_gate_up", t, g.a(g.table(tg)), g.a(g.table(tu)), g.a(g.dev(counts)), g.a(g.dev(xrow)),
+               g.a(g.dev(xin)), g.a(g.dev(win)), 4, 1, rows, cols, g.a(g.dev(q)), g.a(g.dev(d)), g.a(g.dev(scale)), lim,
+               g.a(h), rows, None)
+        got = g.host(h)
+        for m in (0, 2, 3):
+            r = xrow[m]
+            s = xin[r]
+            gg = orc.q8_rows(t, wg[m], rows, cols, q[s:s + 1], d[s:s + 1])[0]
+            uu = orc.q8_rows(t, wu[m], rows, cols, q[s:s + 1], d[s:s + 1])[0]
+            want = np.array([L.orc_lane_swiglu(float(a), float(b), lim, float(scale[win[r]])) for a, b in zip(gg, uu)],
+                            np.float32)
+            assert (g.bits(got[r]) == g.bits(want)).all(), (name, cols, rows, m)
+        assert np.isnan(got[xrow[1]]).all()
