@@ -113,13 +113,17 @@ __device__ __forceinline__ void each8(F&& f) {
 // Q3_K's 8 contract blocks are one 110-byte super-block, 2-aligned: a lane loads the 8 16-byte words that cover it (a
 // buffer descriptor from the matrix's 16-byte-aligned start: words past the end read as zeros) and shifts them in
 // registers to the chunk's first byte (a two-step dword select, then a byte align by 0 or 2)
+// (the same for IQ1_S and IQ1_M, whose 8 blocks are one 50- or 56-byte super-block. measured at one token, us,
+// group_tok_kernel / wide_kernel: IQ1_S 2048 -> 7168 5.74 / 5.19, IQ1_M 6.45 / 5.19; IQ2_XXS 5.47 / 5.90, IQ3_XXS
+// 4096 -> 2048 5.43 / 6.13 and 512 -> 2048 (10 matrices) 6.06 / 6.58 stay with group_tok_kernel - their codebook
+// lookups spread over more lanes there - and so do the types not measured)
 template <uint32_t T>
 constexpr bool wide_serves() {
-  return T == kQ4_0 || T == kQ4_K || T == kQ3_K;
+  return T == kQ4_0 || T == kQ4_K || T == kQ3_K || T == kIQ1_S || T == kIQ1_M;
 }
 template <uint32_t T>
 constexpr uint32_t wide_chunk() {
-  return T == kQ3_K ? 110 : 144;
+  return T == kQ4_0 ? 144 : Block<T>::bytes;
 }
 template <uint32_t T, int L, int R, int NTH>
 __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
@@ -129,6 +133,7 @@ __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restr
   constexpr int RW = NTH / R, nblk = 8 * R, C = L / R, cols = 32 * nblk;
   constexpr uint32_t CB = wide_chunk<T>(), rb = CB * R;
   static_assert(C >= 1 && R <= 32, "a row's lanes within a 32-lane group, chains whole");
+  static_assert(CB % 16 == 0 ? CB == 144 : CB <= 114, "a lane's chunk: nine aligned words, or within 8 words shifted");
   __shared__ __attribute__((aligned(16))) int8_t xq[cols];
   __shared__ float xd[nblk];
   __shared__ __attribute__((aligned(16))) float subs[RW][nblk + 4];  // (+4: the rows' lines on different banks)
@@ -179,7 +184,7 @@ __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restr
     constexpr int b = decltype(bc)::value;
     Codes c;
     if constexpr (T == kQ4_0) codes<T>(RegBytes{W, 18 * b}, 0, c, nullptr);
-    else codes<T>(RegBytes{W, 0}, b, c, nullptr);  // (Q4_K, Q3_K: block b of the super-block)
+    else codes<T>(RegBytes{W, 0}, b, c, const_grid<T>());  // (block b of the super-block)
     int x[8];
     load_x(xq, (uint64_t) (8 * p + b) * 32, x);
     sub[b] = block_sum<T>(c, x);

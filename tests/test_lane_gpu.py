@@ -217,13 +217,13 @@ def test_group_tok_one_token_unaligned_matrix(g, name, cols):
     assert (g.bits(g.host(y)) == g.bits(want)).all()
 
 
-@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q3_K"])
-@pytest.mark.parametrize("cols", [1024, 2048, 4096, 8192])
+@pytest.mark.parametrize("name", ALL_TYPES)
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192])
 def test_group_tok_one_token_wide(g, name, cols):
-    """one token of Q4_0 / Q4_K / Q3_K at the widths whose rows split into runs of 8 contract blocks a lane (144 bytes;
-    Q3_K's 110, shifted into place in registers) over 1024 - 8192 columns, 16 and 32 logical lanes: three matrices in
-    one launch - ragged rows, tokens picked through xin, one matrix with no token (nothing written) - each the
-    oracle's bits"""
+    """one token over 512 - 8192 columns, 16 and 32 logical lanes - for Q4_0, Q4_K, Q3_K, IQ1_S, IQ1_M from 1024 on
+    the runs of 8 contract blocks a lane (Q4_0's 8 blocks and Q4_K's super-block: 144 bytes; the others' super-blocks,
+    50 - 110 bytes, shifted into place in registers), for the rest group_tok_kernel: three matrices in one launch -
+    ragged rows, tokens picked through xin, one matrix with no token (nothing written) - each the oracle's bits"""
     import torch
     t = synth.ID[name]
     rows = 37
