@@ -207,6 +207,54 @@ def deepseek_extras(torch, capi, steps=256):
     return out
 
 
+def engine_step_extras(torch, capi, copies=16):
+    """config 3 at batch 1 through the reference engine's own call sequence (src/run/hip_lane.c: q8_gate_up with each
+    expert's matrices in pointer tables, q8_round of h, q8_group_tok, ops_gather_sum_add), each launch graph-timed on
+    rotated weight copies; the drop-in path for an engine that does not call osmos_lane_layer"""
+    L = capi.lib()
+    k, dim, ff = 10, 2048, 512
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    G = blocks_of(torch, gen, "IQ3_XXS", ff * k, dim, copies)
+    U = blocks_of(torch, gen, "IQ3_XXS", ff * k, dim, copies)
+    D = blocks_of(torch, gen, "IQ3_XXS", dim * k, ff, copies)
+    gb, db = ff * (dim // 256) * 98, dim * (ff // 256) * 98
+    tab = lambda M, b: [torch.tensor([M[c].data_ptr() + e * b for e in range(k)], dtype=torch.int64, device="cuda")  # noqa: E731
+                        for c in range(copies)]
+    tg, tu, td = tab(G, gb), tab(U, gb), tab(D, db)
+    x = torch.randn(1, dim, device="cuda", generator=gen)
+    q = torch.zeros(1, dim, dtype=torch.int8, device="cuda")
+    d = torch.zeros(1, dim // 32, device="cuda")
+    assert L.q8_round(capi.addr(x), 1, dim, dim, capi.addr(q), capi.addr(d), None)
+    cnt = torch.ones(k, dtype=torch.int32, device="cuda")
+    hrow = torch.arange(k, dtype=torch.int32, device="cuda")
+    xin0 = torch.zeros(k, dtype=torch.int32, device="cuda")
+    scale = torch.rand(k, device="cuda", generator=gen)
+    h = torch.zeros(k, ff, device="cuda")
+    hq = torch.zeros(k, ff, dtype=torch.int8, device="cuda")
+    hd = torch.zeros(k, ff // 32, device="cuda")
+    ye = torch.zeros(k, dim, device="cuda")
+    y = torch.zeros(1, dim, device="cuda")
+    add = torch.zeros(1, dim, device="cuda")
+    order = torch.arange(k, dtype=torch.int32, device="cuda")
+    us = {
+        "q8_gate_up": graph_us(torch, lambda i, st: L.q8_gate_up(
+            18, capi.addr(tg[i]), capi.addr(tu[i]), capi.addr(cnt), capi.addr(hrow), capi.addr(xin0), None, k, 1, ff,
+            dim, capi.addr(q), capi.addr(d), capi.addr(scale), math.inf, capi.addr(h), ff, st), copies),
+        "q8_round": graph_us(torch, lambda i, st: L.q8_round(capi.addr(h), k, ff, ff, capi.addr(hq), capi.addr(hd), st),
+                             copies),
+        "q8_group_tok": graph_us(torch, lambda i, st: L.q8_group_tok(
+            18, capi.addr(td[i]), capi.addr(cnt), capi.addr(hrow), None, k, 1, dim, ff, capi.addr(hq), capi.addr(hd),
+            capi.addr(ye), dim, st), copies),
+        "ops_gather_sum_add": graph_us(torch, lambda i, st: L.ops_gather_sum_add(
+            capi.addr(y), capi.addr(ye), capi.addr(order), k, 1, dim, capi.addr(add), st), copies),
+    }
+    total = sum(us.values())
+    nbytes = k * (2 * gb + db) + dim * 5 + dim * 4
+    return {"qwen_engine_step_iq3xxs_bs1": {"us": round(total, 2), "GB/s": round(nbytes / total / 1e3, 1),
+                                             "launches_us": {n: round(v, 2) for n, v in us.items()}}}
+
+
 def roof_frac(us, nbytes, ops, peak_t):
     """the config's roofline time, max(bytes / HBM peak, ops / MFMA peak), over the measured time"""
     return round(max(nbytes / (HBM_PEAK_GBS * 1e3), ops / (peak_t * 1e6)) / us, 4)
@@ -630,6 +678,9 @@ def main():
         torch.cuda.empty_cache()
         extra = {}
         only = set(args.only.split(","))
+        if "3" in only:
+            extra.update(engine_step_extras(torch, capi))
+            torch.cuda.empty_cache()
         for n_tok in (4, 32) if "3" in only else ():
             lb = moe_layer_bench(torch, capi, n_tok, max(args.steps // 4, 64), 16)
             extra["qwen_moe_layer_iq3xxs_bs%d" % n_tok] = {"GB/s": round(lb["gbs"], 2),
