@@ -588,6 +588,28 @@ def ceilings(torch):
                                     "pct_hbm_peak": round(100 * nbytes / us / 1e3 / HBM_PEAK_GBS, 1),
                                     "threads": threads, "unroll": unroll, "workgroups": grid}
         log("read %d B: %.2f us (%d threads x %d, %d workgroups)" % (nbytes, us, threads, unroll, grid))
+    # the routed layer's pattern: 20 regions of 401,408 bytes (10 experts' gate and up, IQ3_XXS 512 x 2048) picked per
+    # launch through a device array of region indices from the pool
+    L.calib_gather.restype = ctypes.c_bool
+    L.calib_gather.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32,
+                               ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    region, n_reg = 401408, 20
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(7)
+    n_slots = pool_bytes // region
+    id_sets = [torch.randperm(n_slots, generator=gen)[:n_reg].to(torch.int32).cuda() for _ in range(32)]
+    best = None
+    for threads, unroll in ((64, 4), (128, 4), (256, 1), (256, 2), (256, 4), (256, 8), (512, 4)):
+        us = graph_us(torch, lambda i, st, threads=threads, unroll=unroll: L.calib_gather(
+            pool.data_ptr(), id_sets[i].data_ptr(), n_reg, region, threads, unroll, sink.data_ptr(), st), 32, reps=5)
+        if best is None or us < best[0]:
+            best = (us, threads, unroll)
+    us, threads, unroll = best
+    nb = region * n_reg
+    out["read"]["gather_20x401408"] = {"us": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                                       "pct_hbm_peak": round(100 * nb / us / 1e3 / HBM_PEAK_GBS, 1),
+                                       "threads": threads, "unroll": unroll}
+    log("gather 20 x 401408 B through device ids: %.2f us (%d threads x %d)" % (us, threads, unroll))
     empty = graph_us(torch, lambda i, st: L.calib_read(pool.data_ptr(), 16, 1, 256, 4, sink.data_ptr(), st), 32)
     out["read"]["one_line_launch_us"] = round(empty, 3)
     blocks, iters = 2048, 4000

@@ -3,6 +3,8 @@
 //   calib_read: a best-shaped streaming read - every thread a run of 16-byte loads, all in flight at once (unrolled),
 //     folded into one word a workgroup so nothing is dead - over `bytes` from `src`: the HBM floor of a launch that
 //     reads that much, for any workgroup size;
+//   calib_gather: the same read over n regions picked through a device array of region indices (the routed layer's
+//     pattern: each expert's matrix one contiguous region, the expert ids read before the weights);
 //   calib_mfma: chains of gfx950 dense MFMAs (int8 16x16x64 / 32x32x32, f16 16x16x32 / 32x32x16), several
 //     independent accumulators a wave so the unit never waits on a result: the matrix cores' measured peak.
 #include <hip/hip_runtime.h>
@@ -29,6 +31,24 @@ __global__ __launch_bounds__(TH) void read_kernel(const u32x4* __restrict__ src,
 #pragma unroll
     for (int u = 0; u < U; u++) acc ^= r[u].x ^ r[u].y ^ r[u].z ^ r[u].w;
   }
+  if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;  // (practically never: keeps the loads live)
+}
+
+// workgroup (x, y): region ids[y] (region_bytes apart from base), its words x TH U .. of (TH U a workgroup)
+template <int TH, int U>
+__global__ __launch_bounds__(TH) void gather_kernel(const uint8_t* __restrict__ base, const int32_t* __restrict__ ids,
+                                                    uint64_t region_bytes, uint32_t* out) {
+  const u32x4* src = (const u32x4*) (base + (uint64_t) (uint32_t) ids[blockIdx.y] * region_bytes);
+  const uint64_t words = region_bytes / 16, b = (uint64_t) blockIdx.x * TH * U;
+  uint32_t acc = 0;
+  u32x4 r[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint64_t i = b + (uint64_t) u * TH + threadIdx.x;
+    r[u] = i < words ? __builtin_nontemporal_load(src + i) : u32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int u = 0; u < U; u++) acc ^= r[u].x ^ r[u].y ^ r[u].z ^ r[u].w;
   if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;  // (practically never: keeps the loads live)
 }
 
@@ -105,6 +125,22 @@ CALIB_API bool calib_read(const void* src, uint64_t bytes, uint32_t grid, uint32
   if (threads == TH && unroll == U) { calib::read_kernel<TH, U><<<grid, TH, 0, s>>>(p, w, out); return hipGetLastError() == hipSuccess; }
   CALIB_R(256, 4) CALIB_R(256, 8) CALIB_R(256, 16) CALIB_R(512, 4) CALIB_R(512, 8) CALIB_R(1024, 4) CALIB_R(1024, 8)
 #undef CALIB_R
+  return false;
+}
+
+CALIB_API bool calib_gather(const void* base, const int32_t* ids, uint32_t n, uint64_t region_bytes, uint32_t threads,
+                            uint32_t unroll, uint32_t* out, void* stream) {
+  if (!base || !ids || !n || !out || region_bytes % 16 || (uintptr_t) base % 16) return false;
+  const hipStream_t s = (hipStream_t) stream;
+  const uint8_t* p = (const uint8_t*) base;
+#define CALIB_G(TH, U)                                                                                      \
+  if (threads == TH && unroll == U) {                                                                       \
+    const dim3 grid((unsigned) ((region_bytes / 16 + TH * U - 1) / (TH * U)), n);                           \
+    calib::gather_kernel<TH, U><<<grid, TH, 0, s>>>(p, ids, region_bytes, out);                           \
+    return hipGetLastError() == hipSuccess;                                                                 \
+  }
+  CALIB_G(64, 4) CALIB_G(128, 4) CALIB_G(256, 1) CALIB_G(256, 2) CALIB_G(256, 4) CALIB_G(256, 8) CALIB_G(512, 4)
+#undef CALIB_G
   return false;
 }
 

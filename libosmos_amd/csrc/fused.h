@@ -104,6 +104,14 @@ struct DnArgs {
 constexpr int kPer = 4;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // (native vectors: kept in registers across waits)
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// a weight word: read once a launch, so a streaming load (no allocation in the caches it would only pass through)
+__device__ __forceinline__ u32x4 wload(const u32x4* p) {
+#ifdef OSM_NO_NT
+  return *p;
+#else
+  return __builtin_nontemporal_load(p);
+#endif
+}
 struct Staged {
   u32x4 v0, v1, v2, v3;
   template <int U>
@@ -135,7 +143,7 @@ __device__ __forceinline__ void stage_load(Staged& st, Src src, uint32_t n, uint
     uint32_t j = (uint32_t) ((float) l * inv);
     j -= j * per_seg > l;
     j += (j + 1) * per_seg <= l;
-    st.template at<u.value>() = ((const u32x4*) src(j))[l - j * per_seg];
+    st.template at<u.value>() = wload((const u32x4*) src(j) + (l - j * per_seg));
   });
 }
 template <int NTH, int S = kPer>
@@ -661,7 +669,7 @@ __device__ __forceinline__ void gu1_item(const GuArgs& a, const G1Tab& tb, uint3
     const u32x4* gsrc = (const u32x4*) (a.gate + (uint64_t) e * a.gate_bytes + (uint64_t) r0 * rb);
     const u32x4* usrc = (const u32x4*) (a.up + (uint64_t) e * a.up_bytes + (uint64_t) r0 * rb);
 #pragma unroll
-    for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = gsrc[idx[u]], wv[S + u] = usrc[idx[u]];
+    for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = wload(gsrc + idx[u]), wv[S + u] = wload(usrc + idx[u]);
   }
   int8_t* q = (int8_t*) (smem + LD::q);
   float* d = (float*) (smem + LD::d);
