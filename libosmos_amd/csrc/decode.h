@@ -97,13 +97,21 @@ __device__ inline void signed_grid(Chunk& c, uint64_t grid, uint32_t signs8) {
   c.w[0] = apply_signs((uint32_t) grid, signs8);
   c.w[1] = apply_signs((uint32_t) (grid >> 32), signs8 >> 4);
 }
-// 4 bytes from a table of int8, indexed by 4 nibbles at `shift` of the bytes of `idx`
-template <typename Tab>
-__device__ inline uint32_t table4(const Tab& K, uint32_t idx, int shift) {
+// the IQ4 non-linear table as 4 little-endian words (entry i at byte i % 4 of word i / 4)
+constexpr uint32_t iq4_word(int w) {
   uint32_t r = 0;
-#pragma unroll
-  for (int b = 0; b < 4; b++) r |= (uint32_t) (uint8_t) K.iq4nl[(idx >> (8 * b + shift)) & 0xF] << (8 * b);
+  for (int b = 0; b < 4; b++) r |= (uint32_t) (uint8_t) make_decode_tables().iq4nl[4 * w + b] << (8 * b);
   return r;
+}
+// 4 bytes from the IQ4 table, indexed by 4 nibbles at `shift` of the bytes of `idx`: entries 0-7 and 8-15 each one
+// byte permute of two table words, then the index's bit 3 picks between them per byte (no memory lookups)
+template <typename Tab>
+__device__ inline uint32_t table4(const Tab&, uint32_t idx, int shift) {
+  const uint32_t n = (idx >> shift) & 0x0F0F0F0Fu, sel = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(iq4_word(1), iq4_word(0), sel);
+  const uint32_t hi = __builtin_amdgcn_perm(iq4_word(3), iq4_word(2), sel);
+  const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
 }
 __device__ inline uint32_t nibbles(uint32_t word, int shift) { return (word >> shift) & (0x0Fu * kEach); }
 __device__ inline float half_at(const uint8_t* p) { return f16(ld16(p)); }

@@ -26,10 +26,14 @@ constexpr int kWaves = 4, kThreads = kWave * kWaves, kHalf = 32;
 // half-wave first copies its row into its own LDS slot with 16-byte loads (a row's bytes in a few wide loads rather
 // than a few bytes a chunk), then decodes the same bytes from there - the same values, so the same bits
 constexpr uint32_t kStgMax = 2048;
-// the types whose decode reads a chunk's bytes in many small pieces (Q4_K / Q5_K's 6-bit scale pairs, IQ1's
-// scattered fields); measured on 8192 x 2048 at one token, staged / not (us): Q4_K 11.0 / 14.8, Q5_K 14.0 / 23.6,
-// IQ1_M 8.1 / 9.1, IQ1_S 7.9 / 8.2; Q4_0, Q2_K, Q3_K, Q6_K, IQ3_XXS and IQ4_XS were 5-20 % slower staged
-template <uint32_t T> constexpr bool stages() { return T == kQ4_K || T == kQ5_K || T == kIQ1_M || T == kIQ1_S; }
+// the types whose decode reads a chunk's bytes in many small pieces (K-quant scale fields, IQ grid indices, sign and
+// scale bytes); measured on 8192 x 2048 at one token, staged / not (us): Q2_K 6.3 / 7.3, Q4_K 7.6 / 9.0, IQ2_XXS 7.0 /
+// 7.6, IQ2_XS 6.9 / 8.0, IQ2_S 7.2 / 10.0, IQ3_XXS 8.4 / 9.8, IQ4_XS 7.1 / 9.0, IQ4_NL 8.0 / 8.9; Q4_0 (8.2 / 7.7)
+// and Q6_K (11.1 / 9.8) were slower staged, Q3_K and Q8_0 even
+template <uint32_t T> constexpr bool stages() {
+  return T == kQ2_K || T == kQ4_K || T == kQ5_K || T == kIQ2_XXS || T == kIQ2_XS || T == kIQ2_S || T == kIQ3_XXS ||
+         T == kIQ1_S || T == kIQ1_M || T == kIQ4_XS || T == kIQ4_NL;
+}
 template <uint32_t T, int NT, int R, bool STG = false>
 __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* __restrict__ x,
                                uint32_t xs, float* __restrict__ y, uint32_t ys, uint32_t live) {
@@ -48,7 +52,7 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
     uint4 r[kStgMax / 16 / kHalf];
 #pragma unroll
     for (int i = 0; i < (int) (kStgMax / 16 / kHalf); i++)
-      if (lane + i * kHalf < (int) words) r[i] = src[lane + i * kHalf];
+      r[i] = src[min((uint32_t) (lane + i * kHalf), words - 1)];  // (every load made: a conditional one puts r in scratch)
 #pragma unroll
     for (int i = 0; i < (int) (kStgMax / 16 / kHalf); i++)
       if (lane + i * kHalf < (int) words) ((uint4*) slot)[lane + i * kHalf] = r[i];
