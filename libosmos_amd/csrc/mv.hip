@@ -27,9 +27,10 @@ constexpr int kWaves = 4, kThreads = kWave * kWaves, kHalf = 32;
 // than a few bytes a chunk), then decodes the same bytes from there - the same values, so the same bits
 constexpr uint32_t kStgMax = 2048;
 // the types whose decode reads a chunk's bytes in many small pieces (K-quant scale fields, IQ grid indices, sign and
-// scale bytes); measured on 8192 x 2048 at one token, staged / not (us): Q2_K 6.3 / 7.3, Q4_K 7.6 / -, IQ2_XXS 7.0 /
-// 7.6, IQ2_XS 6.9 / 8.0, IQ2_S 7.2 / 10.0, IQ3_XXS 8.4 / 9.8, IQ4_XS 7.1 / 9.0, IQ4_NL 8.0 / 8.9; Q4_0 (8.2 / 7.7)
-// and Q6_K (11.1 / 9.8) were slower staged, Q3_K and Q8_0 even
+// scale bytes); measured on 8192 x 2048 at one token, staged / not (us): Q2_K 6.3 / 7.3, IQ2_XXS 7.0 / 7.6, IQ2_XS
+// 6.9 / 8.0, IQ2_S 7.2 / 10.0, IQ3_XXS 8.4 / 9.8, IQ4_XS 12.8 / 14.9 and IQ4_NL 13.0 / 15.6 with the IQ4 table in
+// memory (7.1 and 8.0 staged with it as byte permutes); Q4_K staged 7.6; Q4_0 (8.2 / 7.7) and Q6_K (11.1 / 9.8) were
+// slower staged, Q3_K and Q8_0 even
 template <uint32_t T> constexpr bool stages() {
   return T == kQ2_K || T == kQ4_K || T == kQ5_K || T == kIQ2_XXS || T == kIQ2_XS || T == kIQ2_S || T == kIQ3_XXS ||
          T == kIQ1_S || T == kIQ1_M || T == kIQ4_XS || T == kIQ4_NL;
