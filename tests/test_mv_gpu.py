@@ -123,7 +123,7 @@ def test_refusals(g):
     assert not L.quant_known(99) and L.quant_known(18)
 
 
-@pytest.mark.parametrize("name", ["Q4_K", "IQ1_M"])
+@pytest.mark.parametrize("name", ["Q4_K", "IQ1_M", "IQ2_S", "IQ4_NL"])
 def test_mv_one_token_unaligned_matrix(g, name):
     """one token, a matrix whose start is 8- but not 16-byte aligned: the launch keeps the direct path (the staged
     path copies rows with 16-byte loads and takes only 16-aligned matrices) - the oracle's bits, the same as the
@@ -147,7 +147,8 @@ def test_mv_one_token_unaligned_matrix(g, name):
         assert (g.bits(g.host(y)) == g.bits(want)).all(), what
 
 
-@pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "IQ1_M", "IQ1_S"])
+@pytest.mark.parametrize("name", ["Q2_K", "Q4_K", "Q5_K", "IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ1_M", "IQ1_S",
+                                  "IQ4_XS", "IQ4_NL"])
 def test_mv_group_mixed_alignment(g, name):
     """mv_group over the types whose rows the launch stages through LDS, at cols 2048 (a row a whole number of 16-byte
     words): a table mixing 16-aligned matrices with ones that start 8 bytes past a 16-byte boundary, so one launch
