@@ -222,15 +222,16 @@ __device__ __forceinline__ void one_row(const uint8_t* wm, uint32_t row, uint32_
     __shared__ __attribute__((aligned(16))) uint8_t stg[OneShape<L>::rows][kOneStg];
     uint8_t* slot = stg[threadIdx.x / GL];
     const uint32_t words = (uint32_t) (rb / 16);
-    const uint4* src = (const uint4*) base;
+    typedef uint32_t w4 __attribute__((ext_vector_type(4)));  // (native: an array of HIP's uint4 stays in scratch)
+    const w4* src = (const w4*) base;
     constexpr int kMax = (int) (kOneStg / 16 + GL - 1) / GL;
-    uint4 r[kMax];
+    w4 r[kMax];
 #pragma unroll
     for (int i = 0; i < kMax; i++)
-      if (gl + i * GL < (int) words) r[i] = src[gl + i * GL];
+      r[i] = src[min((uint32_t) (gl + i * GL), words - 1)];  // (every load made: a conditional one puts r in scratch)
 #pragma unroll
-    for (int i = 0; i < kMax; i++)
-      if (gl + i * GL < (int) words) ((uint4*) slot)[gl + i * GL] = r[i];
+    for (int i = 0; i < kMax; i++)  // (past the row's end: its last word again, to the same place - no branches)
+      ((w4*) slot)[min((uint32_t) (gl + i * GL), words - 1)] = r[i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // (the slot is the group's own: no workgroup barrier)
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

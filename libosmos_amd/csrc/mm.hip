@@ -360,6 +360,10 @@ constexpr uint32_t col_tiles(uint32_t n) {
   return t >= 8 ? 8 : t >= 4 ? 4 : t >= 2 ? 2 : 1;
 }
 
+// the 128 x 8 shape (Q8_0, Q6_K, IQ3_XXS) holds a round of 4 slabs' decoded operands: 8 token tiles, or (Q8_0 / Q6_K
+// on 2-byte staging words) 4 row tiles, would need more than 256 VGPRs and spill, so those take 4 token tiles and one
+// row tile
+template <uint32_t SL, int W> constexpr bool heavy() { return SL == 128 && W == 8; }
 template <uint32_t T, uint32_t SL, int W, int CT, int RT>
 bool launch_s(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
   const dim3 grid((a.rows + kTile * RT - 1) / (kTile * RT), n_mat, (max_n + kTile * CT - 1) / (kTile * CT));
@@ -368,8 +372,10 @@ bool launch_s(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
   constexpr uint32_t rbr = SL * W / Block<T>::values * Block<T>::bytes;
   if (row_bytes<T>(a.cols) % 4 == 0 && rbr % 4 == 0)
     kernel<T, SL, W, CT, RT, 4><<<grid, W * kWave, 0, s>>>(a);
-  else
+  else if constexpr (RT == 1 || !heavy<SL, W>() || T == kIQ3_XXS)  // (launch_ct never takes the others)
     kernel<T, SL, W, CT, RT, 2><<<grid, W * kWave, 0, s>>>(a);
+  else
+    return false;
   return hipGetLastError() == hipSuccess;
 }
 
@@ -377,7 +383,9 @@ bool launch_s(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
 // matrices, or a tall one - else 1) and token tiles CT (at most 8 / RT: the accumulators 4 RT CT VGPRs)
 template <uint32_t T, uint32_t SL, int W>
 bool launch_ct(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
-  const bool tall = (uint64_t) n_mat * (a.rows / 64) >= 1024;
+  constexpr uint32_t rbr = SL * W / Block<T>::values * Block<T>::bytes;
+  const bool words2 = row_bytes<T>(a.cols) % 4 != 0 || rbr % 4 != 0;
+  const bool tall = (uint64_t) n_mat * (a.rows / 64) >= 1024 && !(heavy<SL, W>() && T != kIQ3_XXS && words2);
   const uint32_t ct = col_tiles(max_n);
   if (tall) {
     if (ct == 1) return launch_s<T, SL, W, 1, 4>(a, n_mat, max_n, s);
@@ -387,7 +395,7 @@ bool launch_ct(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
     case 1: return launch_s<T, SL, W, 1, 1>(a, n_mat, max_n, s);
     case 2: return launch_s<T, SL, W, 2, 1>(a, n_mat, max_n, s);
     case 4: return launch_s<T, SL, W, 4, 1>(a, n_mat, max_n, s);
-    default: return launch_s<T, SL, W, 8, 1>(a, n_mat, max_n, s);
+    default: return launch_s<T, SL, W, heavy<SL, W>() ? 4 : 8, 1>(a, n_mat, max_n, s);
   }
 }
 

@@ -129,6 +129,47 @@ def test_mm_run_wide(g, name):
     bound_check(name, w, rows, cols, x, y)
 
 
+
+@pytest.mark.parametrize("name", ["Q8_0", "Q6_K", "IQ3_XXS", "Q4_K"])
+def test_mm_many_tokens_and_tall(g, name):
+    """150 tokens (10 token tiles: the widest tiling, which the 128 x 8 K split of Q8_0 / Q6_K / IQ3_XXS caps at 4
+    tiles a workgroup) within the bound and each token's bits its own; then mm_group over 16 matrices of 4096 rows (the
+    4-row-tile form, or for Q6_K's 2-byte staging words - 9 blocks a row - one row tile) - each matrix the bits of
+    mm_run on it alone"""
+    import torch
+    t = synth.ID[name]
+    gen = synth.iq_blocks if name.startswith("IQ") else synth.random_blocks
+    rows, cols = 64, 512
+    w = gen(t, rows, cols, 31)
+    x = np.random.default_rng(12).normal(0, 1, (150, cols)).astype(np.float32)
+    print("mm many tokens", name, flush=True)
+    x16, _ = mm_x16(g, x)
+    y = run(g, name, w, rows, cols, x16, 150)
+    bound_check(name, w, rows, cols, x, y)
+    for k in (0, 77, 149):
+        one16, _ = mm_x16(g, x[k:k + 1])
+        assert (g.bits(run(g, name, w, rows, cols, one16, 1)[0]) == g.bits(y[k])).all(), k
+    # tall: 16 matrices x 64 row blocks of 64 = 1024 row blocks, 3 tokens each
+    n_mat, rows, cols, per = 16, 4096, 2304, 3  # (2304: the tuned K split for mm_run too; 9 blocks a row)
+    mats = [gen(t, rows, cols, 40 + e) for e in range(n_mat)]
+    rng = np.random.default_rng(13)
+    xs = [rng.normal(0, 1, (per, cols)).astype(np.float32) for _ in range(n_mat)]
+    x16 = np.concatenate([x16_layout(xs[e], 16) for e in range(n_mat)])
+    xoff = (np.arange(n_mat) * 16 * cols).astype(np.uint32)
+    yoff = (np.arange(n_mat) * per * rows).astype(np.uint32)
+    cnt = np.full(n_mat, per, np.int32)
+    y = torch.full((n_mat * per, rows), float("nan"), device="cuda")
+    wd = [g.dev(m) for m in mats]
+    x16d = g.dev(x16.view(np.uint16)).view(torch.float16)
+    print("mm tall group", name, flush=True)
+    g.call("mm_group", t, g.a(g.table(wd)), g.a(g.dev(cnt)), n_mat, per, rows, cols, g.a(x16d), g.a(g.dev(xoff)), cols,
+           g.a(y), g.a(g.dev(yoff)), rows, None)
+    got = g.host(y)
+    for e in (0, 7, 15):
+        one16, _ = mm_x16(g, xs[e])
+        alone = run(g, name, mats[e], rows, cols, one16, per)
+        assert (g.bits(got[e * per:(e + 1) * per]) == g.bits(alone)).all(), e
+
 def test_mm_group(g):
     """three experts' gathered tokens (5, 16, 23: whole tiles each) over one x16, outputs at their own offsets: each
     the bits of mm_run on that expert alone; an expert with 0 tokens writes nothing"""
