@@ -360,9 +360,12 @@ constexpr uint32_t col_tiles(uint32_t n) {
   return t >= 8 ? 8 : t >= 4 ? 4 : t >= 2 ? 2 : 1;
 }
 
-// the 128 x 8 shape (Q8_0, Q6_K, IQ3_XXS) holds a round of 4 slabs' decoded operands: 8 token tiles, or (Q8_0 / Q6_K
-// on 2-byte staging words) 4 row tiles, would need more than 256 VGPRs and spill, so those take 4 token tiles and one
-// row tile
+// token tiles a workgroup at most: 2 for a 128-value slab's shapes, 4 for the others. at 8 the 128-value shapes need
+// more than 256 VGPRs (the 128 x 8 of Q8_0 / Q6_K / IQ3_XXS spills, the 128 x 4 of IQ1 / IQ2 runs a wave a SIMD);
+// measured on 2048 -> 7168 at 512 tokens (us, caps 8 / 4 / 2): IQ3_XXS 692 / 147 / 81, IQ2_XXS 318 / 105 / 74,
+// Q8_0 704 / 144 / 104, Q4_K 83 / 69 / 96, Q4_0 88 / 59 / 72, IQ4_XS 88 / 57 / 65. the 128 x 8 shape on 2-byte
+// staging words also spills at 4 row tiles (Q8_0 / Q6_K), so it takes one
+template <uint32_t SL> constexpr int ct_max() { return SL == 128 ? 2 : 4; }
 template <uint32_t SL, int W> constexpr bool heavy() { return SL == 128 && W == 8; }
 template <uint32_t T, uint32_t SL, int W, int CT, int RT>
 bool launch_s(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
@@ -380,7 +383,7 @@ bool launch_s(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
 }
 
 // the tiling: a workgroup's row tiles RT (4 where the launch has row blocks enough for the chip at 64 rows - many
-// matrices, or a tall one - else 1) and token tiles CT (at most 8 / RT: the accumulators 4 RT CT VGPRs)
+// matrices, or a tall one - else 1) and token tiles CT (at most ct_max, and 2 with 4 row tiles)
 template <uint32_t T, uint32_t SL, int W>
 bool launch_ct(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
   constexpr uint32_t rbr = SL * W / Block<T>::values * Block<T>::bytes;
@@ -394,8 +397,7 @@ bool launch_ct(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
   switch (ct) {
     case 1: return launch_s<T, SL, W, 1, 1>(a, n_mat, max_n, s);
     case 2: return launch_s<T, SL, W, 2, 1>(a, n_mat, max_n, s);
-    case 4: return launch_s<T, SL, W, 4, 1>(a, n_mat, max_n, s);
-    default: return launch_s<T, SL, W, heavy<SL, W>() ? 4 : 8, 1>(a, n_mat, max_n, s);
+    default: return launch_s<T, SL, W, ct_max<SL>(), 1>(a, n_mat, max_n, s);
   }
 }
 

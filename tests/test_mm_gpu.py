@@ -132,8 +132,7 @@ def test_mm_run_wide(g, name):
 
 @pytest.mark.parametrize("name", ["Q8_0", "Q6_K", "IQ3_XXS", "Q4_K"])
 def test_mm_many_tokens_and_tall(g, name):
-    """150 tokens (10 token tiles: the widest tiling, which the 128 x 8 K split of Q8_0 / Q6_K / IQ3_XXS caps at 4
-    tiles a workgroup) within the bound and each token's bits its own; then mm_group over 16 matrices of 4096 rows (the
+    """150 tokens (10 token tiles: 2 a workgroup for the 128-value slabs of Q8_0 / Q6_K / IQ3_XXS, 4 for Q4_K's) within the bound and each token's bits its own; then mm_group over 16 matrices of 4096 rows (the
     4-row-tile form, or for Q6_K's 2-byte staging words - 9 blocks a row - one row tile) - each matrix the bits of
     mm_run on it alone"""
     import torch
