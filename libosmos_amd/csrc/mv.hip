@@ -183,13 +183,15 @@ template <int NT> constexpr int rows_per() { return NT == 1 ? 1 : 2; }
 template <uint32_t T, int NT>
 bool run_nt(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t xs, uint32_t n_tok, float* y,
             uint32_t ys, hipStream_t s) {
-  constexpr uint32_t per = kWaves * 2 * rows_per<NT>();
-  const dim3 grid((rows + per - 1) / per, (n_tok + NT - 1) / NT);
   const uint32_t rb = (uint32_t) row_bytes<T>(cols);
-  if (stages<T>() && NT == 1 && rb % 16 == 0 && rb <= kStgMax && (uintptr_t) w % 16 == 0)
-    kernel<T, NT, rows_per<NT>(), NT == 1><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+  auto grid = [&](uint32_t r) { return dim3((rows + kWaves * 2 * r - 1) / (kWaves * 2 * r), (n_tok + NT - 1) / NT); };
+  // (the staged row copy at tiles of up to 4 tokens, one row a half-wave: 2048 -> 6144 Q4_K at 8 tokens 22.1 -> 15.5
+  // us; at tiles of 8 it lost, 60 -> 70 us at 64 tokens)
+  if (stages<T>() && NT <= 4 && rb % 16 == 0 && rb <= kStgMax && (uintptr_t) w % 16 == 0)
+    kernel<T, NT, 1, true><<<grid(1), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
   else
-    kernel<T, NT, rows_per<NT>()><<<grid, kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+    kernel<T, NT, rows_per<NT>()><<<grid(rows_per<NT>()), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs,
+                                                                           n_tok, y, ys);
   return hipGetLastError() == hipSuccess;
 }
 
