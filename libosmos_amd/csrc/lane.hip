@@ -24,6 +24,47 @@ constexpr int kWaves = 4;              // a workgroup's waves
 constexpr int kThreads = kWave * kWaves;
 
 // matrix blockIdx.y: 64 / L rows a wave; logical lane ll its blocks ll, ll + L, ... for each of NT tokens
+// the G row groups of a wave (L logical lanes each) hold the same blocks of different rows, so at a token tile that G
+// divides each group loads the x codes and scales of NT / G of the tile's tokens and lane swaps (v_permlane16_swap,
+// v_permlane32_swap) hand every group all of them: a G-th of the vector-memory work for x (2048 -> 6144 Q3_K at 8
+// tokens 12.4 -> 10.4 us; Q4_K even at 12.1)
+template <int NT, int G> constexpr bool xs_shares() { return NT > 1 && NT % G == 0 && (G == 2 || G == 4); }
+// the x rows of group g's tokens g K + j (selects over the unrolled tokens: no run-time index into xr)
+template <int NT, int G>
+__device__ __forceinline__ void xs_rows(const uint64_t* xr, int g, uint64_t* mr) {
+  constexpr int K = NT / G;
+#pragma unroll
+  for (int j = 0; j < K; j++) {
+    mr[j] = xr[j];
+#pragma unroll
+    for (int t = 1; t < NT; t++)
+      if (t % K == j) mr[j] = g * K + j == t ? xr[t] : mr[j];
+  }
+}
+// block s's x for every token of the tile: xv[t] its 8 code words, then its scale's bits
+template <int NT, int G>
+__device__ __forceinline__ void xs_block(const int8_t* __restrict__ q, const float* __restrict__ d, const uint64_t* mr,
+                                         uint32_t cols, uint32_t nblk, uint32_t s, int (*xv)[9]) {
+  constexpr int K = NT / G;
+#pragma unroll
+  for (int j = 0; j < K; j++) {
+    int w[9];
+    load_x(q, mr[j] * cols + (uint64_t) s * 32, w);
+    w[8] = __float_as_int(d[mr[j] * nblk + s]);
+#pragma unroll
+    for (int e = 0; e < 9; e++) {
+      if constexpr (G == 2) {
+        const auto r = __builtin_amdgcn_permlane32_swap((uint32_t) w[e], (uint32_t) w[e], false, false);
+        xv[j][e] = (int) r[0], xv[K + j][e] = (int) r[1];
+      } else {  // rows of 16 lanes 0 1 2 3: (0 0 2 2 | 1 1 3 3), then each across the halves
+        const auto r = __builtin_amdgcn_permlane16_swap((uint32_t) w[e], (uint32_t) w[e], false, false);
+        const auto u = __builtin_amdgcn_permlane32_swap(r[0], r[0], false, false);
+        const auto v = __builtin_amdgcn_permlane32_swap(r[1], r[1], false, false);
+        xv[j][e] = (int) u[0], xv[K + j][e] = (int) v[0], xv[2 * K + j][e] = (int) u[1], xv[3 * K + j][e] = (int) v[1];
+      }
+    }
+  }
+}
 template <uint32_t T, int NT, int L>
 __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* const* __restrict__ w,
                                                              const int32_t* __restrict__ cnt,
@@ -47,46 +88,17 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   float acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-  // XS: the G row groups of a wave hold the same blocks of different rows, so each loads the x codes and scales of
-  // NT / G of the tile's tokens and lane swaps (v_permlane16_swap, v_permlane32_swap) hand every group all of them:
-  // a G-th of the vector-memory work for x (2048 -> 6144 Q3_K at 8 tokens 12.4 -> 10.4 us; Q4_K even at 12.1)
-  constexpr bool XS = NT > 1 && NT % G == 0 && (G == 2 || G == 4);
-  constexpr int K = XS ? NT / G : 1;  // tokens a group loads
-  uint64_t mr[K];  // the rows of this group's tokens g K + j (selects over the unrolled tokens: no indexed array)
-  if constexpr (XS) {
-    const int g = lane / L;
-#pragma unroll
-    for (int j = 0; j < K; j++) {
-      mr[j] = xr[j];
-#pragma unroll
-      for (int t = 1; t < NT; t++)
-        if (t % K == j) mr[j] = g * K + j == t ? xr[t] : mr[j];
-    }
-  }
+  constexpr bool XS = xs_shares<NT, G>();
+  constexpr int K = XS ? NT / G : 1;
+  uint64_t mr[K];
+  if constexpr (XS) xs_rows<NT, G>(xr, lane / L, mr);
 #pragma unroll(NT == 1 ? 4 : 2)  // (one token: 4 blocks' loads in flight)
   for (uint32_t s = ll; s < nblk; s += L) {
     Codes c;
     codes<T>(rb + (s / per) * Block<T>::bytes, (int) (s % per), c, const_grid<T>());
     if constexpr (XS) {
-      int xv[NT][9];  // token t's 8 code words, then its scale's bits
-#pragma unroll
-      for (int j = 0; j < K; j++) {
-        int w[9];
-        load_x(q, mr[j] * cols + (uint64_t) s * 32, w);
-        w[8] = __float_as_int(d[mr[j] * nblk + s]);
-#pragma unroll
-        for (int e = 0; e < 9; e++) {
-          if constexpr (G == 2) {
-            const auto r = __builtin_amdgcn_permlane32_swap((uint32_t) w[e], (uint32_t) w[e], false, false);
-            xv[j][e] = (int) r[0], xv[K + j][e] = (int) r[1];
-          } else {  // rows of 16 lanes 0 1 2 3: (0 0 2 2 | 1 1 3 3), then each across the halves
-            const auto r = __builtin_amdgcn_permlane16_swap((uint32_t) w[e], (uint32_t) w[e], false, false);
-            const auto u = __builtin_amdgcn_permlane32_swap(r[0], r[0], false, false);
-            const auto v = __builtin_amdgcn_permlane32_swap(r[1], r[1], false, false);
-            xv[j][e] = (int) u[0], xv[K + j][e] = (int) v[0], xv[2 * K + j][e] = (int) u[1], xv[3 * K + j][e] = (int) v[1];
-          }
-        }
-      }
+      int xv[NT][9];
+      xs_block<NT, G>(q, d, mr, cols, nblk, s, xv);
 #pragma unroll
       for (int t = 0; t < NT; t++) acc[t] = __builtin_fmaf(__int_as_float(xv[t][8]), block_sum<T>(c, xv[t]), acc[t]);
     } else {
@@ -351,19 +363,33 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(const uint8_t* const*
   float ag[NT], au[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.0f;
+  constexpr bool XS = xs_shares<NT, G>();
+  uint64_t mr[XS ? NT / G : 1];
+  if constexpr (XS) xs_rows<NT, G>(xr, lane / L, mr);
 #pragma unroll(NT == 1 ? 4 : 2)  // (one token: 4 blocks' loads in flight)
   for (uint32_t s = ll; s < nblk; s += L) {
     Codes cg, cu;
     const uint64_t at = (s / per) * Block<T>::bytes;
     codes<T>(rg + at, (int) (s % per), cg, const_grid<T>());
     codes<T>(ru + at, (int) (s % per), cu, const_grid<T>());
+    if constexpr (XS) {
+      int xv[NT][9];
+      xs_block<NT, G>(q, d, mr, cols, nblk, s, xv);
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      int x[8];
-      load_x(q, xr[t] * cols + (uint64_t) s * 32, x);
-      const float xd = d[xr[t] * nblk + s];
-      ag[t] = __builtin_fmaf(xd, block_sum<T>(cg, x), ag[t]);
-      au[t] = __builtin_fmaf(xd, block_sum<T>(cu, x), au[t]);
+      for (int t = 0; t < NT; t++) {
+        const float xd = __int_as_float(xv[t][8]);
+        ag[t] = __builtin_fmaf(xd, block_sum<T>(cg, xv[t]), ag[t]);
+        au[t] = __builtin_fmaf(xd, block_sum<T>(cu, xv[t]), au[t]);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        int x[8];
+        load_x(q, xr[t] * cols + (uint64_t) s * 32, x);
+        const float xd = d[xr[t] * nblk + s];
+        ag[t] = __builtin_fmaf(xd, block_sum<T>(cg, x), ag[t]);
+        au[t] = __builtin_fmaf(xd, block_sum<T>(cu, x), au[t]);
+      }
     }
   }
 #pragma unroll
