@@ -65,24 +65,14 @@ __device__ __forceinline__ void xs_block(const int8_t* __restrict__ q, const flo
     }
   }
 }
-template <uint32_t T, int NT, int L>
-__global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* const* __restrict__ w,
-                                                             const int32_t* __restrict__ cnt,
-                                                             const int32_t* __restrict__ xrow,
-                                                             const int32_t* __restrict__ xin, uint32_t rows,
-                                                             uint32_t cols, const int8_t* __restrict__ q,
-                                                             const float* __restrict__ d, float* __restrict__ y,
-                                                             uint32_t ys) {
+// a row group's products for the tile's tokens from its row's bytes rb (global memory, or with STG its LDS copy)
+template <uint32_t T, int NT, int L, bool STG>
+__device__ __forceinline__ void tok_rows(const uint8_t* rb, uint32_t row, uint32_t rows, uint32_t cols, uint32_t n,
+                                         uint32_t r0, const int32_t* __restrict__ xin, const int8_t* __restrict__ q,
+                                         const float* __restrict__ d, float* __restrict__ y, uint32_t ys) {
   constexpr int G = kWave / L, per = (int) (Block<T>::values / 32);
   const int lane = threadIdx.x % kWave, ll = lane % L;
-  const uint32_t m = blockIdx.y, row = (blockIdx.x * kWaves + threadIdx.x / kWave) * G + lane / L;
-  // (blockIdx.z: the matrix's token tile, tokens z NT .. z NT + NT - 1 of its cnt[m])
-  const uint32_t n_all = (uint32_t) cnt[m], z0 = blockIdx.z * NT;
-  if (n_all <= z0) return;  // an entry past a device-built table's live ones (osmos_lane_tables), or a tile past its
-                            // tokens: nothing read or written
-  const uint32_t n = n_all - z0 < (uint32_t) NT ? n_all - z0 : NT;
-  const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m] + z0;
-  const uint8_t* rb = w[m] + (uint64_t) (row < rows ? row : 0) * row_bytes<T>(cols);
+  const uint32_t nblk = cols / 32;
   uint64_t xr[NT];
   in_rows<NT>(xin, r0, n, xr);
   float acc[NT];
@@ -115,6 +105,52 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
     const float v = tree<L>(acc[t]);
     if (ll == 0 && row < rows && (uint32_t) t < n) y[(uint64_t) (r0 + t) * ys + row] = v;
   }
+}
+// the types group_tok_kernel stages (its row copied into LDS first): Q4_K, whose decode reads the 6-bit scale fields in
+// small pieces (2048 -> 6144 at 8 tokens 12.3 -> 10.4 us; Q3_K was slower staged, 10.4 -> 11.8)
+template <uint32_t T> constexpr bool tok_stages() { return T == kQ4_K; }
+template <uint32_t T, int NT, int L, bool STG = false>
+__global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* const* __restrict__ w,
+                                                             const int32_t* __restrict__ cnt,
+                                                             const int32_t* __restrict__ xrow,
+                                                             const int32_t* __restrict__ xin, uint32_t rows,
+                                                             uint32_t cols, const int8_t* __restrict__ q,
+                                                             const float* __restrict__ d, float* __restrict__ y,
+                                                             uint32_t ys) {
+  constexpr int G = kWave / L;
+  const int lane = threadIdx.x % kWave, ll = lane % L;
+  const uint32_t m = blockIdx.y, row = (blockIdx.x * kWaves + threadIdx.x / kWave) * G + lane / L;
+  // (blockIdx.z: the matrix's token tile, tokens z NT .. z NT + NT - 1 of its cnt[m])
+  const uint32_t n_all = (uint32_t) cnt[m], z0 = blockIdx.z * NT;
+  if (n_all <= z0) return;  // an entry past a device-built table's live ones (osmos_lane_tables), or a tile past its
+                            // tokens: nothing read or written
+  const uint32_t n = n_all - z0 < (uint32_t) NT ? n_all - z0 : NT;
+  const uint32_t r0 = (uint32_t) xrow[m] + z0;
+  const uint64_t rbytes = row_bytes<T>(cols);
+  const uint8_t* rb = w[m] + (uint64_t) (row < rows ? row : 0) * rbytes;
+  // STG (the matrix 16-aligned, a row a whole number of 16-byte words within a slot: known here, uniform a matrix):
+  // the row group first copies its row into its own LDS slot with 16-byte loads, then decodes from there
+  if constexpr (STG) {
+    constexpr uint32_t kSlot = L == 16 ? 2304 : 4608;  // (Q4_K at 4096 / 8192 columns; 36 KB a workgroup)
+    __shared__ __attribute__((aligned(16))) uint8_t stg[kWaves * G][kSlot];
+    if ((uintptr_t) w[m] % 16 == 0 && rbytes % 16 == 0 && rbytes <= kSlot) {
+      typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+      uint8_t* slot = stg[threadIdx.x / L];
+      const uint32_t words = (uint32_t) (rbytes / 16);
+      constexpr int kMax = (int) (kSlot / 16 + L - 1) / L;
+      w4 r[kMax];
+#pragma unroll
+      for (int i = 0; i < kMax; i++) r[i] = ((const w4*) rb)[min((uint32_t) (ll + i * L), words - 1)];
+#pragma unroll
+      for (int i = 0; i < kMax; i++) ((w4*) slot)[min((uint32_t) (ll + i * L), words - 1)] = r[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // (the slot is the group's own: no workgroup barrier)
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      tok_rows<T, NT, L, true>(slot, row, rows, cols, n, r0, xin, q, d, y, ys);
+      return;
+    }
+  }
+  tok_rows<T, NT, L, false>(rb, row, rows, cols, n, r0, xin, q, d, y, ys);
 }
 
 // one token (q8_group_tok at max_cnt 1, the decode GEMV): a row a group of 2L lanes (a half-wave at 16 logical lanes,
@@ -466,7 +502,7 @@ bool launch(const Args& a, bool fused, hipStream_t s, uint32_t tiles = 1) {
                                                          a.cnt, a.xrow, a.xin, a.win, a.rows, a.cols, a.q, a.d,
                                                          a.scale, a.lim, a.y, a.ys);
   else
-    group_tok_kernel<T, NT, L><<<grid, kThreads, 0, s>>>((const uint8_t* const*) a.wg, a.cnt, a.xrow, a.xin, a.rows,
+    group_tok_kernel<T, NT, L, tok_stages<T>()><<<grid, kThreads, 0, s>>>((const uint8_t* const*) a.wg, a.cnt, a.xrow, a.xin, a.rows,
                                                            a.cols, a.q, a.d, a.y, a.ys);
   return hipGetLastError() == hipSuccess;
 }
