@@ -248,7 +248,7 @@ struct GridStage {
   // expanding: the table's 1024 16-byte words (4 a grid word: its variants 4 q .. 4 q + 3) written in `passes` rounds,
   // word p NTH + threadIdx.x in round p - consecutive lanes, consecutive words (no LDS bank conflicts)
   static constexpr uint32_t passes = 1024 / NTH;
-  static_assert(!expand || NTH >= 256 && NTH <= 1024 && NTH % 256 == 0, "the expansion's thread split");
+  static_assert(!expand || (NTH >= 256 && NTH <= 1024 && NTH % 256 == 0), "the expansion's thread split");
   uint32_t v[expand ? passes : (per > 0 ? per * words : 1)];
 };
 typedef const __attribute__((address_space(1))) uint32_t* gptr32;
