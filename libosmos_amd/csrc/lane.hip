@@ -82,7 +82,8 @@ __device__ __forceinline__ void tok_rows(const uint8_t* rb, uint32_t row, uint32
   constexpr int K = XS ? NT / G : 1;
   uint64_t mr[K];
   if constexpr (XS) xs_rows<NT, G>(xr, lane / L, mr);
-#pragma unroll(NT == 1 ? 4 : 2)  // (one token: 4 blocks' loads in flight)
+#pragma unroll(NT == 1 ? 4 : XS ? 1 : 2)  // (one token: 4 blocks' loads in flight; the swaps are convergent, so a
+                                            // loop holding them stays rolled)
   for (uint32_t s = ll; s < nblk; s += L) {
     Codes c;
     codes<T>(rb + (s / per) * Block<T>::bytes, (int) (s % per), c, const_grid<T>());
@@ -402,7 +403,8 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(const uint8_t* const*
   constexpr bool XS = xs_shares<NT, G>();
   uint64_t mr[XS ? NT / G : 1];
   if constexpr (XS) xs_rows<NT, G>(xr, lane / L, mr);
-#pragma unroll(NT == 1 ? 4 : 2)  // (one token: 4 blocks' loads in flight)
+#pragma unroll(NT == 1 ? 4 : XS ? 1 : 2)  // (one token: 4 blocks' loads in flight; the swaps are convergent, so a
+                                            // loop holding them stays rolled)
   for (uint32_t s = ll; s < nblk; s += L) {
     Codes cg, cu;
     const uint64_t at = (s / per) * Block<T>::bytes;

@@ -76,7 +76,8 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
   for (int q = 0; q < R; q++)
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[q][t] = 0.0f;
-#pragma unroll(NT == 1 ? 8 : 2)  // (one token: the lane's chunks' loads all in flight at once)
+#pragma unroll(NT == 1 ? 8 : SW ? 1 : 2)  // (one token: the lane's chunks' loads all in flight at once; the swaps
+                                          // are convergent, so a loop holding them stays rolled)
   for (uint32_t c = lane; c < chunks; c += kHalf) {
     float v[R][kChunk];
 #pragma unroll
