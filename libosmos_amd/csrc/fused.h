@@ -654,7 +654,7 @@ __device__ __forceinline__ void gu1_item(const GuArgs& a, const G1Tab& tb, uint3
     const uint8_t* ub = tb.wu[m] + (uint64_t) r0 * rb;
     if ((((uintptr_t) gb | (uintptr_t) ub) & 15) == 0) {
 #pragma unroll
-      for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = ((const u32x4*) gb)[idx[u]], wv[S + u] = ((const u32x4*) ub)[idx[u]];
+      for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = wload((const u32x4*) gb + idx[u]), wv[S + u] = wload((const u32x4*) ub + idx[u]);
     } else {  // (a matrix that is not 16-aligned: the same words from two-byte loads)
       auto w16 = [](const uint8_t* p) __attribute__((always_inline)) {
         u32x4 v;
