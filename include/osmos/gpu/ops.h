@@ -26,11 +26,14 @@ bool ops_gather_sum_add(float *y, const float *src, const int32_t *idx, uint32_t
    memory the GPU maps (hipHostMalloc's) - holds value, with or without its top bit (the host's mark of a failed job);
    a system-scope acquire, so what the host wrote before the flag the kernels after see. the lane's hand-off of
    CPU-computed experts (reference src/run/hip_lane.c:218-219). unlike the reference's, the wait is bounded: past
-   osmos_wait_limit (ten minutes unless set) it ends and the next ops_copy_rows writes NaN rows instead of copying (a
-   wait that ends with the value makes copies copy again). false for a value with its top bit set. */
+   osmos_wait_limit (ten minutes unless set) it ends, and the ops_copy_rows queued after it on the same stream write NaN
+   rows instead of copying, until a later wait on that stream ends with its value. the outcome is per (device, stream):
+   waits and copies on other streams do not see it. false for a value with its top bit set (no post can match it: the
+   reference would wait for ever), and once 1023 distinct streams of a device have waited. */
 bool ops_wait(const uint32_t *flag, uint32_t value, void *stream);
 /* replaces reference include/osmos/gpu/ops.h:124 (kernels/ops.hip:884-889): rows idx[0 .. n) of src to the same rows
-   of dst, len floats a row (src may be host memory the GPU maps); NaN rows after an ops_wait that expired */
+   of dst, len floats a row (src may be host memory the GPU maps); NaN rows while the last ops_wait on this stream is
+   one that expired */
 bool ops_copy_rows(float *dst, const float *src, const int32_t *idx, uint32_t n, uint32_t len, void *stream);
 
 #ifdef __cplusplus

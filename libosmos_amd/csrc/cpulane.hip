@@ -13,17 +13,18 @@
 // the row's blocks s go to logical lane s % L (L = 32 from 4096 columns, else 16), fmaf'd onto the lane's sum in
 // order; then the lanes' xor tree. compiled with -ffp-contract=off: every product and sum rounded on its own.
 //
-// the pool: workers asleep between jobs (a condition variable), within a job moving through its four phases together
-// (a spinning barrier: a phase is tens of microseconds); each phase's rows split evenly over the workers - any split
-// gives the same bits, each row's sums its own.
-#include <pthread.h>
+// the pool (described where it is defined, below): a job cut into per-worker slices at submit, the phases joined by a
+// counting latch. any split of the rows gives the same bits: each row's sums are its own.
 #include <sched.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
-#include <cstdlib>
+#include <condition_variable>
 #include <cstring>
-#include <new>
+#include <mutex>
+#include <thread>
+#include <vector>
 
 #include "common.h"
 
@@ -244,9 +245,11 @@ void round_rows(const float* x, uint32_t rows, uint32_t cols, int8_t* q, float* 
   }
 }
 
-// rows r0 .. r1 of a matrix (cols) against cnt rows of codes q / scales d: y[t ys + r]
-void lane_rows(uint32_t type, const void* w, uint32_t cols, uint32_t r0, uint32_t r1, const int8_t* q, const float* d,
+// rows r0 .. r1 of a matrix (cols) against cnt rows of codes q / scales d: y[t ys + r]; false (nothing written) for
+// a type that is not the lane's or cols not whole 256-value blocks
+bool lane_rows(uint32_t type, const void* w, uint32_t cols, uint32_t r0, uint32_t r1, const int8_t* q, const float* d,
                uint32_t cnt, float* y, uint32_t ys) {
+  if (!lane_type(type) || !cols || cols % 256 || r1 < r0) return false;
   const uint32_t nblk = cols / 32, L = cols >= 4096 ? 32 : 16;
   const uint64_t rb = (uint64_t) (cols / block_values(type)) * block_bytes(type);
   for (uint32_t r = r0; r < r1; r++) {
@@ -264,6 +267,7 @@ void lane_rows(uint32_t type, const void* w, uint32_t cols, uint32_t r0, uint32_
       y[(uint64_t) t * ys + r] = acc[0];
     }
   }
+  return true;
 }
 
 float lane_exp(float x) {
@@ -294,202 +298,232 @@ float lane_swiglu(float g, float u, float lim, float scale) {
 
 using namespace osm;
 
+// ---- the pool ----
+//
+// A job is cut into work before any worker sees it: cpu_lane_submit lays each phase's rows out as per-worker slices
+// (the x rows and the activation rows as contiguous row ranges; the gate/up rows and the down rows as runs of
+// (expert, first row, last row) over the experts' matrices laid end to end, balanced to within one row). The workers
+// then only run their own slices. Between phases they meet at a counting latch: one atomic counts every worker's
+// finished phases in this job, and phase p is over for everyone once it reaches (p + 1) * workers; the worker whose
+// increment ends the last phase posts the job's value. Between jobs the workers sleep on a condition variable keyed
+// by a job serial, which also orders the plan's writes before their reads.
+namespace {
+
+struct Slice {
+  uint32_t e, r0, r1;  // rows r0 .. r1 of the job's expert e
+};
+struct WorkerPlan {
+  uint32_t x0 = 0, x1 = 0;  // x rows to round (and, with ff, the activation rows to round)
+  std::vector<Slice> gu, dn;
+};
+
+constexpr uint32_t kPhases = 4;  // x rounded; gate, up, SwiGLU; activations rounded; down
+
+}  // namespace
+
 struct CpuLane {
-  int n = 0;
-  pthread_t th[CPU_LANE_THREADS_MAX];
   uint32_t max_rows = 0, dim = 0, ff = 0;
-  int8_t *q = nullptr, *qh = nullptr;  // x's rows, then the activations, as int8
-  float *qd = nullptr, *qhd = nullptr;  // their blocks' scales
-  float *g = nullptr, *u = nullptr, *h = nullptr;
-  pthread_mutex_t mu;
-  pthread_cond_t wake, idle;
+  std::vector<int8_t> xq, hq;   // the job's x rows, then its activations, as int8 codes
+  std::vector<float> xs, hs;    // their 32-value blocks' scales
+  std::vector<float> gate, up, act;
+  std::vector<std::thread> workers;
+  std::vector<WorkerPlan> plan;
   CpuLaneJob job{};
-  uint64_t gen = 0;
-  bool busy = false, quit = false, all_ok = true;  // (mu's)
-  std::atomic<int> left{0}, arrived{0};
-  std::atomic<bool> failed{false};
-  std::atomic<unsigned> phase{0};
+  std::mutex mu;
+  std::condition_variable start, done;
+  uint64_t issued = 0, finished = 0;  // jobs (mu's)
+  bool stopping = false, clean = true;  // (mu's) clean: no job failed since the last wait
+  std::atomic<uint32_t> latch{0};
+  std::atomic<bool> bad{false};
 };
 
 namespace {
 
-struct WorkerArg {
-  CpuLane* c;
-  int id;
-  int core;
-};
-
-void spin_barrier(CpuLane* c) {
-  const unsigned ph = c->phase.load(std::memory_order_acquire);
-  if (c->arrived.fetch_add(1, std::memory_order_acq_rel) + 1 == c->n) {
-    c->arrived.store(0, std::memory_order_relaxed);
-    c->phase.store(ph + 1, std::memory_order_release);
-    return;
+// `total` rows of `rows`-row matrices laid end to end, cut into `n` runs of near-equal length: run w into plan[w]
+void cut_rows(uint32_t n_e, uint32_t rows, std::vector<WorkerPlan>& plan, std::vector<Slice> WorkerPlan::*list) {
+  const uint64_t total = (uint64_t) n_e * rows, n = plan.size();
+  uint32_t e = 0, r = 0;
+  for (uint64_t w = 0; w < n; w++) {
+    std::vector<Slice>& out = plan[w].*list;
+    out.clear();
+    for (uint64_t want = total / n + (w < total % n ? 1 : 0); want;) {
+      const uint32_t take = (uint32_t) std::min<uint64_t>(want, rows - r);
+      out.push_back({e, r, r + take});
+      want -= take, r += take;
+      if (r == rows) e++, r = 0;
+    }
   }
-  while (c->phase.load(std::memory_order_acquire) == ph) {
+}
+
+bool job_ok(const CpuLane* c, const CpuLaneJob* j) {
+  if (!j->x || !j->scale || !j->e || !j->y || !j->seq || !j->n_e || !j->n_rows) return false;
+  if (!cpu::lane_type(j->type_gu) || !cpu::lane_type(j->type_down)) return false;
+  if (j->dim != c->dim || j->ff != c->ff || j->n_rows > c->max_rows) return false;
+  for (const CpuLaneExpert* x = j->e; x != j->e + j->n_e; x++)
+    if (!x->gate || !x->up || !x->down || !x->cnt || (uint64_t) x->row0 + x->cnt > j->n_rows) return false;
+  return true;
+}
+
+// every worker has finished `phases` phases of this job
+void meet(CpuLane* c, uint32_t phases) {
+  const uint32_t goal = phases * (uint32_t) c->workers.size();
+  c->latch.fetch_add(1, std::memory_order_acq_rel);
+  while (c->latch.load(std::memory_order_acquire) < goal) {
 #if defined(__x86_64__)
     __builtin_ia32_pause();
 #endif
   }
 }
 
-void share(int id, int n, uint64_t total, uint64_t* a, uint64_t* b) {
-  *a = total * (uint64_t) id / (uint64_t) n, *b = total * (uint64_t) (id + 1) / (uint64_t) n;
-}
-
-// the experts' rows laid end to end (`rows` each): fn(expert, r0, r1) over rows a .. b of them
-template <typename F>
-void over_parts(const CpuLaneJob& j, uint32_t rows, uint64_t a, uint64_t b, F fn) {
-  for (uint32_t k = (uint32_t) (a / rows); k < j.n_e && (uint64_t) k * rows < b; k++) {
-    const uint64_t lo = (uint64_t) k * rows, r0 = a > lo ? a - lo : 0, r1 = b < lo + rows ? b - lo : rows;
-    fn(j.e[k], (uint32_t) r0, (uint32_t) r1);
-  }
-}
-
-void run_job(CpuLane* c, int id) {
+void run_plan(CpuLane* c, const WorkerPlan& p) {
   const CpuLaneJob& j = c->job;
   const uint32_t D = j.dim, F = j.ff;
-  for (uint32_t r = (uint32_t) id; r < j.n_rows; r += (uint32_t) c->n)  // x's rows rounded
-    cpu::round_rows(j.x + (uint64_t) r * D, 1, D, c->q + (uint64_t) r * D, c->qd + (uint64_t) r * (D / 32));
-  spin_barrier(c);
-  uint64_t a, b;
-  share(id, c->n, (uint64_t) j.n_e * F, &a, &b);  // gate and up rows, the activation
-  over_parts(j, F, a, b, [&](const CpuLaneExpert& e, uint32_t r0, uint32_t r1) {
-    const int8_t* q = c->q + (uint64_t) e.row0 * D;
-    const float* qd = c->qd + (uint64_t) e.row0 * (D / 32);
-    float *g = c->g + (uint64_t) e.row0 * F, *u = c->u + (uint64_t) e.row0 * F, *h = c->h + (uint64_t) e.row0 * F;
-    cpu::lane_rows(j.type_gu, e.gate, D, r0, r1, q, qd, e.cnt, g, F);
-    cpu::lane_rows(j.type_gu, e.up, D, r0, r1, q, qd, e.cnt, u, F);
-    for (uint32_t t = 0; t < e.cnt; t++)
-      for (uint32_t r = r0; r < r1; r++) {
-        const uint64_t i = (uint64_t) t * F + r;
-        h[i] = cpu::lane_swiglu(g[i], u[i], j.lim, j.scale[e.row0 + t]);
-      }
-  });
-  spin_barrier(c);
-  for (uint32_t r = (uint32_t) id; r < j.n_rows; r += (uint32_t) c->n)  // the activations rounded
-    cpu::round_rows(c->h + (uint64_t) r * F, 1, F, c->qh + (uint64_t) r * F, c->qhd + (uint64_t) r * (F / 32));
-  spin_barrier(c);
-  share(id, c->n, (uint64_t) j.n_e * D, &a, &b);  // down rows
-  over_parts(j, D, a, b, [&](const CpuLaneExpert& e, uint32_t r0, uint32_t r1) {
-    cpu::lane_rows(j.type_down, e.down, F, r0, r1, c->qh + (uint64_t) e.row0 * F, c->qhd + (uint64_t) e.row0 * (F / 32),
-                   e.cnt, j.y + (uint64_t) e.row0 * D, D);
-  });
+  bool ok = true;
+  cpu::round_rows(j.x + (uint64_t) p.x0 * D, p.x1 - p.x0, D, c->xq.data() + (uint64_t) p.x0 * D,
+                  c->xs.data() + (uint64_t) p.x0 * (D / 32));
+  meet(c, 1);
+  for (const Slice& s : p.gu) {
+    const CpuLaneExpert& e = j.e[s.e];
+    const uint64_t xo = (uint64_t) e.row0 * D, ho = (uint64_t) e.row0 * F;
+    ok &= cpu::lane_rows(j.type_gu, e.gate, D, s.r0, s.r1, c->xq.data() + xo, c->xs.data() + xo / 32, e.cnt,
+                         c->gate.data() + ho, F);
+    ok &= cpu::lane_rows(j.type_gu, e.up, D, s.r0, s.r1, c->xq.data() + xo, c->xs.data() + xo / 32, e.cnt,
+                         c->up.data() + ho, F);
+    for (uint32_t t = 0; t < e.cnt; t++) {
+      const float w = j.scale[e.row0 + t];
+      for (uint64_t i = ho + (uint64_t) t * F + s.r0; i < ho + (uint64_t) t * F + s.r1; i++)
+        c->act[i] = cpu::lane_swiglu(c->gate[i], c->up[i], j.lim, w);
+    }
+  }
+  meet(c, 2);
+  cpu::round_rows(c->act.data() + (uint64_t) p.x0 * F, p.x1 - p.x0, F, c->hq.data() + (uint64_t) p.x0 * F,
+                  c->hs.data() + (uint64_t) p.x0 * (F / 32));
+  meet(c, 3);
+  for (const Slice& s : p.dn) {
+    const CpuLaneExpert& e = j.e[s.e];
+    const uint64_t ho = (uint64_t) e.row0 * F;
+    ok &= cpu::lane_rows(j.type_down, e.down, F, s.r0, s.r1, c->hq.data() + ho, c->hs.data() + ho / 32, e.cnt,
+                         j.y + (uint64_t) e.row0 * D, D);
+  }
+  if (!ok) c->bad.store(true, std::memory_order_relaxed);
 }
 
-void* worker(void* p) {
-  WorkerArg arg = *(WorkerArg*) p;
-  delete (WorkerArg*) p;
-  CpuLane* c = arg.c;
-  uint64_t seen = 0;
-  for (;;) {
-    pthread_mutex_lock(&c->mu);
-    while (c->gen == seen && !c->quit) pthread_cond_wait(&c->wake, &c->mu);
-    if (c->quit) {
-      pthread_mutex_unlock(&c->mu);
-      return nullptr;
+void finish_job(CpuLane* c) {
+  const bool failed = c->bad.load(std::memory_order_relaxed);
+  __atomic_store_n(c->job.seq, c->job.value | (failed ? CPU_LANE_FAILED : 0u), __ATOMIC_RELEASE);
+  std::lock_guard<std::mutex> lk(c->mu);
+  c->clean = c->clean && !failed;
+  c->finished++;
+  c->done.notify_all();
+}
+
+void worker_main(CpuLane* c, size_t id) {
+  for (uint64_t next = 1;; next++) {
+    {
+      std::unique_lock<std::mutex> lk(c->mu);
+      c->start.wait(lk, [&] { return c->stopping || c->issued >= next; });
+      if (c->stopping) return;
     }
-    seen = c->gen;
-    pthread_mutex_unlock(&c->mu);
-    run_job(c, arg.id);
-    if (c->left.fetch_sub(1, std::memory_order_acq_rel) == 1) {  // the last one done: post, then the pool idle
-      const bool failed = c->failed.load(std::memory_order_relaxed);
-      __atomic_store_n(c->job.seq, c->job.value | (failed ? CPU_LANE_FAILED : 0u), __ATOMIC_RELEASE);
-      pthread_mutex_lock(&c->mu);
-      c->all_ok = c->all_ok && !failed, c->busy = false;
-      pthread_cond_broadcast(&c->idle);
-      pthread_mutex_unlock(&c->mu);
-    }
+    run_plan(c, c->plan[id]);
+    const uint32_t all = kPhases * (uint32_t) c->workers.size();
+    if (c->latch.fetch_add(1, std::memory_order_acq_rel) + 1 == all) finish_job(c);
   }
 }
 
-bool job_ok(const CpuLane* c, const CpuLaneJob* j) {
-  if (!cpu::lane_type(j->type_gu) || !cpu::lane_type(j->type_down) || j->dim != c->dim || j->ff != c->ff || !j->x ||
-      !j->scale || !j->e || !j->n_e || !j->y || !j->seq || !j->n_rows || j->n_rows > c->max_rows)
-    return false;
-  for (uint32_t k = 0; k < j->n_e; k++)
-    if (!j->e[k].gate || !j->e[k].up || !j->e[k].down || !j->e[k].cnt || j->e[k].row0 + j->e[k].cnt > j->n_rows)
-      return false;
-  return true;
+// the calling thread onto CPU `core` (before it runs anything else)
+bool pin_self(int core) {
+  if (core < 0 || core >= CPU_SETSIZE) return false;
+  cpu_set_t set;
+  CPU_ZERO(&set);
+  CPU_SET(core, &set);
+  return sched_setaffinity(0, sizeof set, &set) == 0;
 }
 
 }  // namespace
 
 extern "C" OSM_API CpuLane* cpu_lane_create(int threads, const int* cores, uint32_t max_rows, uint32_t dim, uint32_t ff) {
   if (threads < 1 || threads > CPU_LANE_THREADS_MAX || !max_rows || !dim || dim % 256 || !ff || ff % 256) return nullptr;
-  CpuLane* c = new (std::nothrow) CpuLane;
-  if (!c) return nullptr;
-  c->max_rows = max_rows, c->dim = dim, c->ff = ff;
-  const uint64_t rd = (uint64_t) max_rows * dim, rf = (uint64_t) max_rows * ff;
-  c->q = (int8_t*) std::malloc(rd), c->qh = (int8_t*) std::malloc(rf);
-  c->qd = (float*) std::malloc(rd / 32 * 4), c->qhd = (float*) std::malloc(rf / 32 * 4);
-  c->g = (float*) std::malloc(rf * 4), c->u = (float*) std::malloc(rf * 4), c->h = (float*) std::malloc(rf * 4);
-  pthread_mutex_init(&c->mu, nullptr), pthread_cond_init(&c->wake, nullptr), pthread_cond_init(&c->idle, nullptr);
-  if (!c->q || !c->qh || !c->qd || !c->qhd || !c->g || !c->u || !c->h) {
-    cpu_lane_destroy(c);
+  CpuLane* c = nullptr;
+  // each worker pins itself first and reports; create returns only once all have (or one could not)
+  std::mutex m;
+  std::condition_variable cv;
+  int reported = 0;
+  bool pinned = true;
+  try {
+    c = new CpuLane;
+    c->max_rows = max_rows, c->dim = dim, c->ff = ff;
+    const uint64_t rd = (uint64_t) max_rows * dim, rf = (uint64_t) max_rows * ff;
+    c->xq.resize(rd), c->hq.resize(rf), c->xs.resize(rd / 32), c->hs.resize(rf / 32);
+    c->gate.resize(rf), c->up.resize(rf), c->act.resize(rf);
+    c->plan.resize((size_t) threads);
+    c->workers.reserve((size_t) threads);
+    for (int i = 0; i < threads; i++)
+      c->workers.emplace_back([c, i, cores, &m, &cv, &reported, &pinned] {
+        const bool ok = !cores || pin_self(cores[i]);
+        {
+          std::lock_guard<std::mutex> lk(m);
+          pinned = pinned && ok, reported++;
+          cv.notify_all();
+        }
+        worker_main(c, (size_t) i);
+      });
+    std::unique_lock<std::mutex> lk(m);
+    cv.wait(lk, [&] { return reported == threads; });
+    if (!pinned) {
+      lk.unlock();
+      cpu_lane_destroy(c);
+      return nullptr;
+    }
+    return c;
+  } catch (...) {  // memory or a thread refused: the workers already started are joined
+    if (c) {
+      std::unique_lock<std::mutex> lk(m);
+      cv.wait(lk, [&] { return reported == (int) c->workers.size(); });
+      lk.unlock();
+      cpu_lane_destroy(c);
+    }
     return nullptr;
   }
-  for (int i = 0; i < threads; i++) {
-    pthread_attr_t at;
-    if (pthread_attr_init(&at)) {
-      cpu_lane_destroy(c);
-      return nullptr;
-    }
-    bool ok = true;
-    if (cores) {  // pinned from its first instruction: the attributes carry the CPU (one the kernel refuses: none)
-      cpu_set_t set;
-      CPU_ZERO(&set);
-      ok = cores[i] >= 0 && cores[i] < CPU_SETSIZE;
-      if (ok) CPU_SET(cores[i], &set);
-      ok = ok && pthread_attr_setaffinity_np(&at, sizeof set, &set) == 0;
-    }
-    WorkerArg* a = ok ? new (std::nothrow) WorkerArg{c, i, cores ? cores[i] : -1} : nullptr;
-    ok = a && pthread_create(&c->th[i], &at, worker, a) == 0;
-    pthread_attr_destroy(&at);
-    if (!ok) {
-      delete a;
-      cpu_lane_destroy(c);
-      return nullptr;
-    }
-    c->n = i + 1;
-  }
-  return c;
 }
 
 extern "C" OSM_API void cpu_lane_destroy(CpuLane* c) {
   if (!c) return;
   cpu_lane_wait(c);
-  pthread_mutex_lock(&c->mu);
-  c->quit = true;
-  pthread_cond_broadcast(&c->wake);
-  pthread_mutex_unlock(&c->mu);
-  for (int i = 0; i < c->n; i++) pthread_join(c->th[i], nullptr);
-  pthread_mutex_destroy(&c->mu), pthread_cond_destroy(&c->wake), pthread_cond_destroy(&c->idle);
-  std::free(c->q), std::free(c->qh), std::free(c->qd), std::free(c->qhd), std::free(c->g), std::free(c->u),
-      std::free(c->h);
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->stopping = true;
+    c->start.notify_all();
+  }
+  for (std::thread& t : c->workers) t.join();
   delete c;
 }
 
 extern "C" OSM_API bool cpu_lane_submit(CpuLane* c, const CpuLaneJob* job) {
   if (!c || !job || !job_ok(c, job)) return false;
-  pthread_mutex_lock(&c->mu);
-  const bool free_ = !c->busy;
-  if (free_) {
-    c->job = *job, c->busy = true, c->gen++;
-    c->failed.store(false, std::memory_order_relaxed);
-    c->left.store(c->n, std::memory_order_release);
-    pthread_cond_broadcast(&c->wake);
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (c->finished != c->issued) return false;  // a job under way
+  try {
+    const uint64_t n = c->plan.size();
+    for (uint64_t w = 0; w < n; w++)
+      c->plan[w].x0 = (uint32_t) (job->n_rows * w / n), c->plan[w].x1 = (uint32_t) (job->n_rows * (w + 1) / n);
+    cut_rows(job->n_e, job->ff, c->plan, &WorkerPlan::gu);
+    cut_rows(job->n_e, job->dim, c->plan, &WorkerPlan::dn);
+  } catch (...) {
+    return false;
   }
-  pthread_mutex_unlock(&c->mu);
-  return free_;
+  c->job = *job;
+  c->latch.store(0, std::memory_order_relaxed);
+  c->bad.store(false, std::memory_order_relaxed);
+  c->issued++;
+  c->start.notify_all();
+  return true;
 }
 
 extern "C" OSM_API bool cpu_lane_wait(CpuLane* c) {
   if (!c) return false;
-  pthread_mutex_lock(&c->mu);
-  while (c->busy) pthread_cond_wait(&c->idle, &c->mu);
-  const bool ok = c->all_ok;
-  c->all_ok = true;
-  pthread_mutex_unlock(&c->mu);
+  std::unique_lock<std::mutex> lk(c->mu);
+  c->done.wait(lk, [&] { return c->finished == c->issued; });
+  const bool ok = c->clean;
+  c->clean = true;
   return ok;
 }

@@ -8,6 +8,9 @@
 // sigmoid-gated shared expert), reference include/osmos/gpu/ops.h:311-355 and kernels/ops.hip:502-525 (swiglu_lane,
 // gather_rows, gather_sum_add), reference src/run/hip_lane.c:115-200 (the lane's entries and token order).
 #include <atomic>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "common.h"
 
@@ -86,68 +89,142 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* __res
 }
 
 // ---- q4x_expert_tiles ----
-__device__ inline int run_of(int c) { return c <= 16 ? 0 : c <= 32 ? 1 : c <= 64 ? 2 : 3; }
+// One workgroup builds the tables in three passes, each over the outputs it writes:
+//   1. per-expert figures: a count histogram, then one record per expert - its places (its picks), its slots (picks
+//      rounded up to tiles of 16) and its entries in each of the Q4X_TILE_RUNS runs - prefix-summed by a two-level
+//      wave scan (a wave's 64 experts by cross-lane shifts, then the 16 waves' totals by one wave);
+//   2. entry-major: every entry index of every run, up to the run's bound, is one thread's; it finds its expert by a
+//      binary search over that run's prefix, works out which part of the expert it is, and writes the part (or cnt 0
+//      past the run's live entries);
+//   3. slot-major: every slot index up to the slot bound is one thread's; padding slots (past an expert's picks or
+//      past the last expert's tiles) get -1. The live slots are written by the pick placement: with n <= 1024 picks,
+//      in this workgroup, each pick ranking itself among the earlier picks of its expert; beyond that, by
+//      place_kernel (a workgroup an expert).
+constexpr int kTileThreads = 1024, kTileWaves = kTileThreads / kWave, kRecs = 2 + Q4X_TILE_RUNS;
+constexpr uint32_t kPlaceInline = 1024;
 
-constexpr int kTileThreads = 1024, kScans = 2 + Q4X_TILE_RUNS;  // places, slots, each run's entries
-constexpr uint32_t kPlaceInline = 256;
+// which run a part of m tokens (1 .. kPart) belongs to: tiles of 1, 2, 4 or 8
+__device__ inline int part_run(int m) { return m > 64 ? 3 : m > 32 ? 2 : m > 16 ? 1 : 0; }
 
-// expert e's own share of scan a: its picks, its slots (whole tiles), its entries in run r
-__device__ inline int own(int c, int a) {
-  if (a == 0) return c;
-  if (a == 1) return (c + kTile - 1) / kTile * kTile;
-  const int r = a - 2, rem = c % kPart;
-  return (r == Q4X_TILE_RUNS - 1 ? c / kPart : 0) + (rem && run_of(rem) == r);
+// expert record field f for an expert of c picks
+__device__ inline int rec_field(int c, int f) {
+  if (f == 0) return c;
+  if (f == 1) return (c + kTile - 1) & ~(kTile - 1);
+  const int full = c / kPart, tail = c - full * kPart, r = f - 2;
+  int n = tail && part_run(tail) == r;
+  if (r == Q4X_TILE_RUNS - 1) n += full;
+  return n;
+}
+
+// index of the first element of the ascending inclusive prefix `inc[0 .. n)` that exceeds v
+__device__ inline int first_above(const int* inc, int n, int v) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (inc[mid] > v) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
 }
 
 __global__ __launch_bounds__(kTileThreads) void tiles_kernel(const int32_t* __restrict__ ids, uint32_t n, uint32_t k,
                                                              uint32_t n_exp, uint32_t dim, uint32_t ff,
                                                              Q4xExpertTiles t, Q4xExpertBounds bd) {
-  __shared__ int count[kMaxExperts], sc[kScans][kMaxExperts], total[kScans];
-  const uint32_t e = threadIdx.x;  // a thread an expert (n_exp <= 1024)
-  if (e < n_exp) count[e] = 0;
+  __shared__ int hist[kMaxExperts];
+  __shared__ int inc[kRecs][kMaxExperts];  // inclusive prefix of each record field over experts
+  __shared__ int wsum[kRecs][kTileWaves];
+  __shared__ int pick_id[kPlaceInline];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  hist[tid] = 0;
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < n; i += kTileThreads) atomicAdd(&count[ids[i]], 1);
-  __syncthreads();
-  const int c = e < n_exp ? count[e] : 0;
-  for (int a = 0; a < kScans; a++) sc[a][e] = e < n_exp ? own(c, a) : 0;
-  __syncthreads();
-  for (uint32_t d = 1; d < kMaxExperts; d <<= 1) {  // inclusive scans (Hillis-Steele) over the 1024 places
-    int v[kScans];
-    for (int a = 0; a < kScans; a++) v[a] = e >= d ? sc[a][e - d] : 0;
-    __syncthreads();
-    for (int a = 0; a < kScans; a++) sc[a][e] += v[a];
-    __syncthreads();
+  const bool inline_place = n <= kPlaceInline;
+  for (uint32_t i = tid; i < n; i += kTileThreads) {
+    const int e = ids[i];
+    if (inline_place) pick_id[i] = e;
+    atomicAdd(&hist[e], 1);
   }
-  if (threadIdx.x < (uint32_t) kScans) total[threadIdx.x] = sc[threadIdx.x][kMaxExperts - 1];
   __syncthreads();
-  if (e < n_exp) {
-    int ex[kScans];
-    for (int a = 0; a < kScans; a++) ex[a] = sc[a][e] - own(c, a);
-    t.off[e] = ex[0], t.off[n_exp + e] = ex[1], t.off[2 * n_exp + e] = c;
-    if (c) {
-      const int p0 = ex[0], s0 = ex[1];
-      if (n <= kPlaceInline) {  // this expert's picks in pick order
-        int q = p0;
-        for (uint32_t i = 0; i < n && q < p0 + c; i++)
-          if (ids[i] == (int32_t) e) t.where[i] = q, t.gidx[s0 + q - p0] = (int32_t) (i / k), t.hidx[s0 + q - p0] = q, q++;
+
+  // pass 1: thread tid is expert tid (experts past n_exp count 0)
+  const int c = hist[tid];
+  int v[kRecs];
+#pragma unroll
+  for (int f = 0; f < kRecs; f++) {
+    v[f] = rec_field(c, f);
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(v[f], d, kWave);
+      if (lane >= d) v[f] += o;
+    }
+    if (lane == kWave - 1) wsum[f][wave] = v[f];
+  }
+  __syncthreads();
+  if (wave == 0) {  // the waves' totals, exclusive, in place
+#pragma unroll
+    for (int f = 0; f < kRecs; f++) {
+      const int s = lane < kTileWaves ? wsum[f][lane] : 0;
+      int x = s;
+#pragma unroll
+      for (int d = 1; d < kTileWaves; d <<= 1) {
+        const int o = __shfl_up(x, d, kWave);
+        if (lane >= d) x += o;
       }
-      for (int s = s0 + c; s < s0 + own(c, 1); s++) t.gidx[s] = -1, t.hidx[s] = -1;
-      int at[Q4X_TILE_RUNS];
-      for (int r = 0; r < Q4X_TILE_RUNS; r++) at[r] = (int) bd.first[r] + ex[2 + r];
-      for (int part = 0; part * kPart < c; part++) {
-        const int m = c - part * kPart < kPart ? c - part * kPart : kPart, en = at[run_of(m)]++;
-        const int slot = s0 + part * kPart, place = p0 + part * kPart;
-        t.cnt[en] = m;
-        t.xg[en] = (uint32_t) slot * dim, t.xd[en] = (uint32_t) slot * ff;
-        t.yg[en] = (uint32_t) place * ff, t.yd[en] = (uint32_t) place * dim;
-        for (int j = 0; j < Q4X_GROUP_TENSORS; j++)
-          t.ptr[j][en] = t.tab[j] ? t.tab[j][e] : (const uint8_t*) t.base[j] + (uint64_t) e * t.bytes[j];
+      if (lane < kTileWaves) wsum[f][lane] = x - s;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int f = 0; f < kRecs; f++) inc[f][tid] = v[f] + wsum[f][wave];
+  __syncthreads();
+
+  const int place0 = inc[0][tid] - c, slot0 = inc[1][tid] - rec_field(c, 1);
+  if ((uint32_t) tid < n_exp) t.off[tid] = place0, t.off[n_exp + tid] = slot0, t.off[2 * n_exp + tid] = c;
+
+  // pass 2: entries
+  for (int r = 0; r < Q4X_TILE_RUNS; r++) {
+    const int live = inc[2 + r][kMaxExperts - 1];
+    for (uint32_t i = tid; i < bd.count[r]; i += kTileThreads) {
+      const uint32_t en = bd.first[r] + i;
+      if ((int) i >= live) {
+        t.cnt[en] = 0;
+        continue;
+      }
+      const int e = first_above(inc[2 + r], kMaxExperts, (int) i);
+      const int ce = hist[e], li = (int) i - (inc[2 + r][e] - rec_field(ce, 2 + r));
+      const int part = r == Q4X_TILE_RUNS - 1 ? li : ce / kPart;  // runs 0-2 hold only an expert's short last part
+      const int m = min(kPart, ce - part * kPart);
+      const uint32_t slot = (uint32_t) (inc[1][e] - rec_field(ce, 1) + part * kPart);
+      const uint32_t place = (uint32_t) (inc[0][e] - ce + part * kPart);
+      t.cnt[en] = m;
+      t.xg[en] = slot * dim, t.xd[en] = slot * ff, t.yg[en] = place * ff, t.yd[en] = place * dim;
+      for (int j = 0; j < Q4X_GROUP_TENSORS; j++) {
+        const void* mat = t.tab[j] ? (const void*) t.tab[j][e] : (const void*) ((const uint8_t*) t.base[j] + (uint64_t) e * t.bytes[j]);
+        t.ptr[j][en] = mat;
       }
     }
   }
-  for (int r = 0; r < Q4X_TILE_RUNS; r++)
-    for (uint32_t i = (uint32_t) total[2 + r] + threadIdx.x; i < bd.count[r]; i += kTileThreads) t.cnt[bd.first[r] + i] = 0;
-  for (uint32_t s = (uint32_t) total[1] + threadIdx.x; s < bd.slots; s += kTileThreads) t.gidx[s] = -1, t.hidx[s] = -1;
+
+  // pass 3: padding slots
+  const int live_slots = inc[1][kMaxExperts - 1];
+  for (uint32_t s = tid; s < bd.slots; s += kTileThreads) {
+    bool pad = (int) s >= live_slots;
+    if (!pad) {
+      const int e = first_above(inc[1], kMaxExperts, (int) s);
+      pad = (int) s - (inc[1][e] - rec_field(hist[e], 1)) >= hist[e];
+    }
+    if (pad) t.gidx[s] = -1, t.hidx[s] = -1;
+  }
+
+  // the placement of small steps: pick i's place is its expert's first plus the earlier picks of that expert
+  if (inline_place)
+    for (uint32_t i = tid; i < n; i += kTileThreads) {
+      const int e = pick_id[i];
+      int before = 0;
+      for (uint32_t j = 0; j < i; j++) before += pick_id[j] == e;
+      const int q = inc[0][e] - hist[e] + before;
+      const int s = inc[1][e] - rec_field(hist[e], 1) + before;
+      t.where[i] = q, t.gidx[s] = (int32_t) (i / k), t.hidx[s] = q;
+    }
 }
 
 // a workgroup an expert: its picks placed in pick order, a tile of 256 picks at a time (a wave's ballot prefix, then
@@ -210,36 +287,39 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(float* __restrict__ ds
 
 // the stream held until *flag (host memory the GPU maps) holds value, with or without its top bit (the host's mark of
 // a failed job) - one thread polling it with system-scope acquire loads (vector loads: never the scalar cache, which
-// would not see the host's store), a sleep between polls. the wait is bounded by the wall clock (s_memrealtime's 100
-// MHz counter; the reference waits without bound, kernels/ops.hip:878-882): past `limit` ticks it gives up and sets
-// `expired`, which makes the next row copy write NaN rows rather than rows the host never wrote; a wait that ends
-// with the value clears it
-__device__ uint32_t expired = 0;
-__global__ __launch_bounds__(64) void wait_kernel(const uint32_t* flag, uint32_t value, uint64_t limit) {
+// would not see the host's store), a short sleep (2 x 64 clocks) between polls. the wait is bounded by the wall clock
+// (s_memrealtime's 100 MHz counter; the reference waits without bound, kernels/ops.hip:878-882): past `limit` ticks it
+// gives up. Its outcome goes to the expiry word of its stream (expiry[slot], one word a (device, stream) pair, given
+// out by the host on the stream's first wait), and the copies queued after it on that stream read that word: NaN rows
+// after a wait that expired, the host's rows after one that saw its value. Other streams' waits and copies touch
+// other words. Slot 0 is never waited on: copies on a stream that never waited always copy.
+constexpr int kExpirySlots = 1024;
+__device__ uint32_t expiry[kExpirySlots];
+__global__ __launch_bounds__(64) void wait_kernel(const uint32_t* flag, uint32_t value, uint64_t limit, uint32_t slot) {
   if (threadIdx.x) return;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t out = 0;
   for (;;) {
     const uint32_t v = __hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-    if ((v & 0x7FFFFFFFu) == value) {
-      __hip_atomic_store(&expired, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
+    if ((v & 0x7FFFFFFFu) == value) break;
     if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
-      __hip_atomic_store(&expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
+      out = 1;
+      break;
     }
-    __builtin_amdgcn_s_sleep(64);
+    __builtin_amdgcn_s_sleep(2);
   }
+  __hip_atomic_store(&expiry[slot], out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // rows idx[0 .. n) of src copied to the same rows of dst, len floats a row (src may be mapped host memory); NaN rows
-// instead after a wait that expired
+// instead after a wait on this stream that expired
 __global__ __launch_bounds__(256) void copy_rows_kernel(float* __restrict__ dst, const float* __restrict__ src,
-                                                        const int32_t* __restrict__ idx, uint32_t n, uint32_t len) {
+                                                        const int32_t* __restrict__ idx, uint32_t n, uint32_t len,
+                                                        uint32_t slot) {
   const uint64_t i = (uint64_t) blockIdx.x * 256 + threadIdx.x;
   if (i < (uint64_t) n * len) {
     const uint64_t at = (uint64_t) idx[i / len] * len + i % len;
-    dst[at] = __hip_atomic_load(&expired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? __builtin_nanf("") : src[at];
+    dst[at] = __hip_atomic_load(&expiry[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? __builtin_nanf("") : src[at];
   }
 }
 
@@ -418,22 +498,43 @@ extern "C" OSM_API bool ops_gather_rows(float* dst, const float* src, const int3
 
 namespace {
 std::atomic<uint64_t> wait_limit_ticks{600ull * 100000000ull};  // (ten minutes of the 100 MHz counter)
+
+// the expiry word of each (device, stream) pair that has waited: slot 1 .. kExpirySlots - 1, given out in order
+std::mutex slot_mu;
+std::map<std::pair<int, uintptr_t>, uint32_t> slot_of;
+uint32_t slots_used[64];  // by device
+
+// the stream's slot; with `give`, one is given out on its first call (0: none left, or no device)
+uint32_t stream_slot(void* stream, bool give) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lk(slot_mu);
+  const auto key = std::make_pair(dev, (uintptr_t) stream);
+  const auto it = slot_of.find(key);
+  if (it != slot_of.end()) return it->second;
+  if (!give || slots_used[dev] + 1 >= (uint32_t) moe::kExpirySlots) return 0;
+  return slot_of[key] = ++slots_used[dev];
 }
+}  // namespace
 
 extern "C" OSM_API void osmos_wait_limit(uint64_t us) {
   wait_limit_ticks.store(us ? us * 100ull : 600ull * 100000000ull, std::memory_order_relaxed);
 }
 
 extern "C" OSM_API bool ops_wait(const uint32_t* flag, uint32_t value, void* stream) {
-  if (!flag || (value & 0x80000000u)) return false;  // (a value with the failed mark's bit: not one a job posts)
-  moe::wait_kernel<<<1, 64, 0, (hipStream_t) stream>>>(flag, value, wait_limit_ticks.load(std::memory_order_relaxed));
+  if (!flag || (value & 0x80000000u)) return false;  // (a value with the failed mark's bit: no post could match it)
+  const uint32_t slot = stream_slot(stream, true);
+  if (!slot) return false;  // (more streams have waited on this device than there are expiry words)
+  moe::wait_kernel<<<1, 64, 0, (hipStream_t) stream>>>(flag, value, wait_limit_ticks.load(std::memory_order_relaxed),
+                                                      slot);
   return hipGetLastError() == hipSuccess;
 }
 
 extern "C" OSM_API bool ops_copy_rows(float* dst, const float* src, const int32_t* idx, uint32_t n, uint32_t len,
                                       void* stream) {
   if (!dst || !src || !idx || !n || !len) return false;
-  moe::copy_rows_kernel<<<moe::grid256((uint64_t) n * len), 256, 0, (hipStream_t) stream>>>(dst, src, idx, n, len);
+  moe::copy_rows_kernel<<<moe::grid256((uint64_t) n * len), 256, 0, (hipStream_t) stream>>>(
+      dst, src, idx, n, len, stream_slot(stream, false));
   return hipGetLastError() == hipSuccess;
 }
 

@@ -108,3 +108,32 @@ def test_cpu_lane_refusals():
         assert L.cpu_lane_wait(pool)
     finally:
         L.cpu_lane_destroy(pool)
+
+
+def test_cpu_lane_pinned_and_repeated():
+    """workers pinned to given CPUs (a CPU that cannot be taken refuses the pool); one pool, several jobs in a row,
+    each flag posted with its own value and the oracle's bits; more workers than rows"""
+    import os
+    L = capi.lib()
+    assert not L.cpu_lane_create(2, (ctypes.c_int * 2)(0, -1), 4, 512, 256)
+    cpus = sorted(os.sched_getaffinity(0))[:3]
+    pool = L.cpu_lane_create(len(cpus), (ctypes.c_int * len(cpus))(*cpus), 8, 512, 256)
+    assert pool
+    try:
+        t = synth.ID["IQ3_XXS"]
+        for rep, cnt in enumerate(([1], [2, 1, 3], [1, 1])):
+            gate, up, down, x, scale, row0, cn = make_job(t, t, 512, 256, len(cnt), cnt, 50 + rep)
+            want = oracle_rows(t, t, 512, 256, 2.0, gate, up, down, x, scale, row0, cn)
+            es = (capi.CpuLaneExpert * len(cnt))(*[capi.CpuLaneExpert(gate[e].ctypes.data, up[e].ctypes.data,
+                                                                      down[e].ctypes.data, int(row0[e]), int(cn[e]))
+                                                   for e in range(len(cnt))])
+            y = np.full((x.shape[0], 512), np.nan, np.float32)
+            seq = np.zeros(1, np.uint32)
+            job = capi.CpuLaneJob(t, t, 512, 256, 2.0, x.ctypes.data, scale.ctypes.data, x.shape[0], es, len(cnt),
+                                  y.ctypes.data, seq.ctypes.data, 100 + rep)
+            assert L.cpu_lane_submit(pool, ctypes.byref(job))
+            assert L.cpu_lane_wait(pool)
+            assert int(seq[0]) == 100 + rep
+            assert (bits(y) == bits(want)).all(), rep
+    finally:
+        L.cpu_lane_destroy(pool)

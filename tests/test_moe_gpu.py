@@ -76,10 +76,14 @@ def tiles_ref(ids, k, n_exp, dim, ff, bases, nbytes):
 
 
 def test_expert_tiles(g):
+    """the tables at decode, mid and prefill sizes (the in-workgroup placement up to 1024 picks, the per-expert one
+    beyond), experts at a base + stride or through an address table, and the scratch's per-expert figures"""
     import torch
     rng = np.random.default_rng(2)
-    for n_tok, k, n_exp in [(3, 10, 512), (512, 8, 256), (40, 4, 64)]:
-        if n_tok == 512:  # Zipf(1.1) load skew, distinct experts a token
+    cases = [(3, 10, 512, False), (512, 8, 256, False), (40, 4, 64, True), (100, 8, 256, False), (128, 8, 256, True),
+             (129, 8, 256, False), (300, 10, 1024, True), (1, 1, 1, False)]
+    for n_tok, k, n_exp, use_tab in cases:
+        if n_tok >= 128:  # Zipf(1.1) load skew, distinct experts a token
             p = 1.0 / np.arange(1, n_exp + 1) ** 1.1
             p /= p.sum()
             ids = np.concatenate([rng.choice(n_exp, k, replace=False, p=p) for _ in range(n_tok)]).astype(np.int32)
@@ -87,21 +91,37 @@ def test_expert_tiles(g):
             ids = np.concatenate([rng.choice(n_exp, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
         n = len(ids)
         dim, ff = 2048, 512
-        bases, nbytes = [0x10000000, 0x20000000, 0x30000000], [4096, 4096, 8192]
+        if use_tab:  # experts anywhere: a scattered table of addresses per tensor
+            tabs = [(rng.integers(1, 1 << 40, n_exp) * 256).astype(np.int64) for _ in range(3)]
+            bases, nbytes = [0, 0, 0], [0, 0, 0]
+        else:
+            tabs = None
+            bases, nbytes = [0x10000000, 0x20000000, 0x30000000], [4096, 4096, 8192]
         bd, where, gidx, hidx, entries = tiles_ref(ids, k, n_exp, dim, ff, bases, nbytes)
+        if use_tab:
+            for r in range(4):
+                entries[r] = [(m, a, b, c, d, [int(tabs[j][e]) for j in range(3)])
+                              for (m, a, b, c, d, _), e in zip(entries[r], tiles_experts(ids, n_exp, r))]
         E, S = bd.entries, bd.slots
-        T = lambda m, dt=torch.int32: torch.full((m,), -7, dtype=dt, device="cuda")  # noqa: E731
+        T = lambda m, dt=torch.int32: torch.full((max(m, 1),), -7, dtype=dt, device="cuda")  # noqa: E731
         cnt, gi, hi, wh, off = T(E), T(S), T(S), T(n), T(3 * n_exp)
         xg, yg, xd, yd = (T(E, torch.int32) for _ in range(4))
-        ptrs = [torch.zeros(E, dtype=torch.int64, device="cuda") for _ in range(3)]
+        ptrs = [torch.zeros(max(E, 1), dtype=torch.int64, device="cuda") for _ in range(3)]
+        dtabs = [torch.from_numpy(tb).cuda() for tb in tabs] if use_tab else None
         t = capi.Q4xExpertTiles()
         for j in range(3):
-            t.base[j], t.bytes[j], t.tab[j], t.ptr[j] = bases[j], nbytes[j], None, ptrs[j].data_ptr()
+            t.base[j], t.bytes[j], t.ptr[j] = bases[j], nbytes[j], ptrs[j].data_ptr()
+            t.tab[j] = dtabs[j].data_ptr() if use_tab else None
         t.cnt, t.gidx, t.hidx, t.where, t.off = cnt.data_ptr(), gi.data_ptr(), hi.data_ptr(), wh.data_ptr(), off.data_ptr()
         t.xg, t.yg, t.xd, t.yd = xg.data_ptr(), yg.data_ptr(), xd.data_ptr(), yd.data_ptr()
         g.call("q4x_expert_tiles", g.a(g.dev(ids)), n, k, n_exp, dim, ff, ctypes.byref(t), None)
-        assert (g.host(wh) == where).all()
-        assert (g.host(gi) == gidx).all() and (g.host(hi) == hidx).all()
+        assert (g.host(wh) == where).all(), n
+        assert (g.host(gi)[:S] == gidx).all() and (g.host(hi)[:S] == hidx).all(), n
+        count = np.bincount(ids, minlength=n_exp)
+        oh = g.host(off)
+        assert (oh[2 * n_exp:] == count).all()
+        assert (oh[:n_exp] == np.concatenate([[0], np.cumsum(count)[:-1]])).all()
+        assert (oh[n_exp:2 * n_exp] == np.concatenate([[0], np.cumsum((count + 15) // 16 * 16)[:-1]])).all()
         ch = g.host(cnt)
         host = {nm: g.host(v).astype(np.int64) for nm, v in [("xg", xg), ("xd", xd), ("yg", yg), ("yd", yd)]}
         ph = [g.host(p_) for p_ in ptrs]
@@ -111,11 +131,24 @@ def test_expert_tiles(g):
                 en = bd.first[r] + i
                 if i < len(live):
                     m, a, b, c, d, pp = live[i]
-                    assert ch[en] == m and host["xg"][en] == a and host["xd"][en] == b
-                    assert host["yg"][en] == c and host["yd"][en] == d
-                    assert [ph[j][en] for j in range(3)] == pp
+                    assert ch[en] == m and host["xg"][en] == a and host["xd"][en] == b, (n, r, i)
+                    assert host["yg"][en] == c and host["yd"][en] == d, (n, r, i)
+                    assert [int(ph[j][en]) for j in range(3)] == pp, (n, r, i)
                 else:
-                    assert ch[en] == 0
+                    assert ch[en] == 0, (n, r, i)
+
+
+def tiles_experts(ids, n_exp, r):
+    """the expert of each live entry of run r, in entry order"""
+    count = np.bincount(ids, minlength=n_exp)
+    out = []
+    for e in range(n_exp):
+        c = int(count[e])
+        for part in range((c + 127) // 128):
+            m = min(128, c - part * 128)
+            if (0 if m <= 16 else 1 if m <= 32 else 2 if m <= 64 else 3) == r:
+                out.append(e)
+    return out
 
 
 def test_moe_sum_and_ops(g):

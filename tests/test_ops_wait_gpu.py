@@ -88,3 +88,40 @@ def test_wait_bound_then_nan_rows():
     torch.cuda.synchronize()
     assert (dst.cpu().numpy()[[1, 5]] == 3.0).all()
     assert not L.ops_wait(capi.addr(flag), 9 | (1 << 31), None)  # a value with the mark's bit: refused
+
+
+def test_expiry_is_per_stream():
+    """two flags on two streams: the wait on stream A expires (A's copies write NaN) while the wait on stream B sees its
+    value (B's copies copy), and a third stream that never waited copies; then B expires and A's next wait succeeds,
+    each stream's copies following its own wait only"""
+    import torch
+    L = capi.lib()
+    fa = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    fb = torch.full((1,), 4, dtype=torch.int32, pin_memory=True)
+    n = 64
+    src = torch.full((4, n), 2.0, pin_memory=True)
+    idx = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device="cuda")
+    sa, sb, sc = torch.cuda.Stream(), torch.cuda.Stream(), torch.cuda.Stream()
+    print("ops_wait per stream", flush=True)
+
+    def step(wa, wb):
+        da, db, dc = (torch.zeros(4, n, device="cuda") for _ in range(3))
+        torch.cuda.synchronize()
+        assert L.ops_wait(capi.addr(fa), wa, sa.cuda_stream)
+        sa.synchronize()
+        assert L.ops_wait(capi.addr(fb), wb, sb.cuda_stream)
+        sb.synchronize()
+        for d, s in ((da, sa), (db, sb), (dc, sc)):
+            assert L.ops_copy_rows(capi.addr(d), capi.addr(src), capi.addr(idx), 4, n, s.cuda_stream)
+        torch.cuda.synchronize()
+        return da.cpu().numpy(), db.cpu().numpy(), dc.cpu().numpy()
+
+    L.osmos_wait_limit(2000)
+    try:
+        a, b, c = step(9, 4)  # A's flag never posts 9: expires; B's holds 4
+        assert np.isnan(a).all() and (b == 2.0).all() and (c == 2.0).all()
+        fa.fill_(9)
+        a, b, c = step(9, 5)  # now A sees its value, B expires
+        assert (a == 2.0).all() and np.isnan(b).all() and (c == 2.0).all()
+    finally:
+        L.osmos_wait_limit(0)
