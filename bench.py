@@ -255,6 +255,26 @@ def engine_step_extras(torch, capi, copies=16):
                                              "launches_us": {n: round(v, 2) for n, v in us.items()}}}
 
 
+SIMDS, CLOCK_GHZ = 1024, 2.4  # MI355X: 256 CUs x 4 SIMDs; a wave64 VALU instruction issues in 4 cycles of a SIMD
+
+
+def contract_floor(outputs, groups, valu_per=4):
+    """the bit-exact contract's own VALU floor: every (output, 32-value group) takes `valu_per` VALU operations that
+    no reassociation may merge (mmq: the group's product, the dot's conversion and two fma; the lane: the two half
+    products, their sum and the chain's fma), 64 lanes a wave instruction, 4 cycles each on one of 1024 SIMDs at
+    2.4 GHz: returns (wave instructions, microseconds)"""
+    winst = outputs * groups * valu_per / 64.0
+    return winst, winst * 4 / (SIMDS * CLOCK_GHZ * 1e3)
+
+
+def with_floor(entry, outputs, groups):
+    winst, floor = contract_floor(outputs, groups)
+    entry["contract_valu_winst_M"] = round(winst / 1e6, 1)
+    entry["contract_floor_us"] = round(floor, 1)
+    entry["frac_of_contract_floor"] = round(floor / entry["us"], 3)
+    return entry
+
+
 def roof_frac(us, nbytes, ops, peak_t):
     """the config's roofline time, max(bytes / HBM peak, ops / MFMA peak), over the measured time"""
     return round(max(nbytes / (HBM_PEAK_GBS * 1e3), ops / (peak_t * 1e6)) / us, 4)
@@ -309,10 +329,10 @@ def prefill_extras(torch, capi):
                                                    capi.addr(soff_d), capi.addr(y), capi.addr(yoff_d), rows, st), 4)
     tops = 2.0 * rows * cols * pairs_n / us / 1e6
     nbytes = int((cnt > 0).sum()) * rows * (cols // 256) * 144 + slots * cols * 9 // 8 + pairs_n * rows * 4
-    out["prefill_q4k_down_mmq_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
-                                        "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
-                                        "roofline_frac": roof_frac(us, nbytes, 2.0 * rows * cols * pairs_n,
-                                                                   INT8_PEAK_TOPS)}
+    out["prefill_q4k_down_mmq_int8"] = with_floor(
+        {"us": round(us, 1), "TOPS": round(tops, 2), "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
+         "roofline_frac": roof_frac(us, nbytes, 2.0 * rows * cols * pairs_n, INT8_PEAK_TOPS)},
+        pairs_n * rows, cols // 32)
     # the dense sub-shape: one Q4_K expert 2048 -> 7168 over all 512 tokens (32 full tiles: no padded slots) - the
     # compute-bound case of the same kernel
     idx1 = torch.arange(n_tok, dtype=torch.int32, device="cuda")
@@ -328,10 +348,10 @@ def prefill_extras(torch, capi):
                                                    capi.addr(x8d), capi.addr(dxd), capi.addr(sxd), capi.addr(z),
                                                    capi.addr(yd), capi.addr(z), rows, st), 8)
     tops = 2.0 * rows * cols * n_tok / us / 1e6
-    out["dense_q4k_down_mmq_int8_512tok"] = {
+    out["dense_q4k_down_mmq_int8_512tok"] = with_floor({
         "us": round(us, 2), "TOPS": round(tops, 2), "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
         "roofline_frac": roof_frac(us, rows * (cols // 256) * 144 + n_tok * cols * 9 // 8 + n_tok * rows * 4,
-                                   2.0 * rows * cols * n_tok, INT8_PEAK_TOPS)}
+                                   2.0 * rows * cols * n_tok, INT8_PEAK_TOPS)}, n_tok * rows, cols // 32)
     del W, wt, x8, dx, sx, y, x8d, dxd, sxd, yd
     torch.cuda.empty_cache()
     # IQ2_XXS gate on f16 MFMA: rows 2048, cols 7168
@@ -366,11 +386,11 @@ def prefill_extras(torch, capi):
                                                           int(cnt.max()), rows, cols, capi.addr(q8), capi.addr(d8),
                                                           capi.addr(y), rows, st), 4)
     tops = 2.0 * rows * cols * pairs_n / us / 1e6
-    out["prefill_iq2xxs_gate_lane_int8"] = {"us": round(us, 1), "TOPS": round(tops, 2),
-                                            "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
-                                            "roofline_frac": roof_frac(us, wbytes + pairs_n * cols * 9 // 8
-                                                                       + pairs_n * rows * 4,
-                                                                       2.0 * rows * cols * pairs_n, INT8_PEAK_TOPS)}
+    out["prefill_iq2xxs_gate_lane_int8"] = with_floor(
+        {"us": round(us, 1), "TOPS": round(tops, 2), "pct_int8_mfma_peak": round(100 * tops / INT8_PEAK_TOPS, 3),
+         "roofline_frac": roof_frac(us, wbytes + pairs_n * cols * 9 // 8 + pairs_n * rows * 4,
+                                    2.0 * rows * cols * pairs_n, INT8_PEAK_TOPS)},
+        pairs_n * rows, cols // 32)
     del W, wt, x16, y
     torch.cuda.empty_cache()
     return out
@@ -484,9 +504,34 @@ def half_bench(torch, capi, lay, half, reps=20):
     return dict(us=us, bytes=nbytes, gbs=nbytes / (us * 1e-6) / 1e9)
 
 
+def llc_bytes():
+    """the host's last-level cache in bytes, summed over the distinct caches the process's CPUs share (sysfs); 0 if
+    unknown"""
+    seen, total = set(), 0
+    for c in sorted(os.sched_getaffinity(0)):
+        base = "/sys/devices/system/cpu/cpu%d/cache" % c
+        try:
+            idx = max((int(d[5:]) for d in os.listdir(base) if d.startswith("index")), default=None)
+            if idx is None:
+                continue
+            with open("%s/index%d/shared_cpu_list" % (base, idx)) as f:
+                key = (idx, f.read().strip())
+            if key in seen:
+                continue
+            seen.add(key)
+            with open("%s/index%d/size" % (base, idx)) as f:
+                v = f.read().strip()
+            total += int(v[:-1]) * {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}[v[-1]] if v[-1] in "KMG" else int(v)
+        except (OSError, ValueError):
+            continue
+    return total
+
+
 def cpu_baseline(lay, seconds=10.0):
     """the reference's CPU path on this host's cores for one step of the same layer (bs as the GPU's), a bounded
-    sample: repetitions of the layer until ~`seconds` of CPU time"""
+    sample: repetitions of the layer until ~`seconds` of CPU time, cold: the repetitions rotate through copies of the
+    step's expert weights (the same bytes at other addresses) totalling at least four times the host's last-level
+    cache, so each step reads its weights from DRAM as a decode step does"""
     import numpy as np
     from oracle import orc
     torch = __import__("torch")
@@ -502,6 +547,11 @@ def cpu_baseline(lay, seconds=10.0):
     mats = {}
     for nm, t in zip(("g", "u", "d"), lyr.tensors):
         mats[nm] = [t[e].cpu().numpy() for e in experts]
+    step_bytes = len(experts) * lay["per_expert"] + n_tok * dim * 8
+    llc = llc_bytes()
+    copies = max(4, -(-4 * max(llc, 256 << 20) // max(step_bytes, 1)))
+    copies = min(copies, max(1, int(4e9 // step_bytes)))
+    rot = {nm: [np.copy(m) for _ in range(copies) for m in ms] for nm, ms in mats.items()}
     pairs = sorted((int(ids[t, j]), t * k + j) for t in range(n_tok) for j in range(k))
     r0 = np.array([min(r for r, (e, _) in enumerate(pairs) if e == ex) for ex in experts], np.uint32)
     cnt = np.array([sum(1 for e, _ in pairs if e == ex) for ex in experts], np.uint32)
@@ -509,48 +559,57 @@ def cpu_baseline(lay, seconds=10.0):
     rows_x = np.stack([x[m // k] for _, m in pairs]).astype(np.float32)
     scale = lay["w"][0].cpu().numpy().reshape(-1)[[m for _, m in pairs]].astype(np.float32)
     P = ctypes.c_void_p
-    tab = lambda ms: (P * len(experts))(*[m.ctypes.data for m in ms])  # noqa: E731
+    tab = lambda ms: (P * len(ms))(*[m.ctypes.data for m in ms])  # noqa: E731
     threads = len(os.sched_getaffinity(0))
     y = np.zeros((len(pairs), dim), np.float32)
     if kind == "reference":
         q, d = orc.q8_round(rows_x, R)
-        args = (18, dim, ff, tab(mats["g"]), tab(mats["u"]), tab(mats["d"]), orc.ptr(r0), orc.ptr(cnt), len(experts),
-                len(pairs), orc.ptr(q), orc.ptr(d), orc.ptr(scale), orc.ptr(y), threads)
-        assert R.ref_lane_layer_mt(*args, 3)  # warm-up
+        tg, tu, td = tab(rot["g"]), tab(rot["u"]), tab(rot["d"])
+
+        def run(th, reps):
+            assert R.ref_lane_layer_rot(18, dim, ff, tg, tu, td, orc.ptr(r0), orc.ptr(cnt), len(experts), len(pairs),
+                                        orc.ptr(q), orc.ptr(d), orc.ptr(scale), orc.ptr(y), th, reps, copies)
+            return
+
+        run(threads, copies)  # warm-up: one pass over every copy (page faults, thread start)
         t0 = time.perf_counter()
-        assert R.ref_lane_layer_mt(*args, 10)
+        run(threads, 10)
         per = (time.perf_counter() - t0) / 10
-        reps = max(10, int(seconds / max(per, 1e-6)))
+        reps = max(copies, int(seconds / max(per, 1e-6)))
         t0 = time.perf_counter()
-        assert R.ref_lane_layer_mt(*args, reps)
+        run(threads, reps)
         per = (time.perf_counter() - t0) / reps
         # one core as well (the same layer, a quarter of the sample's time)
-        args1 = args[:-1] + (1,)
         t0 = time.perf_counter()
-        assert R.ref_lane_layer_mt(*args1, 1)
+        run(1, 1)
         per1 = time.perf_counter() - t0
         reps1 = max(2, int(seconds / 4 / max(per1, 1e-6)))
         t0 = time.perf_counter()
-        assert R.ref_lane_layer_mt(*args1, reps1)
+        run(1, reps1)
         per1 = (time.perf_counter() - t0) / reps1
     else:
         threads = 1
         t0 = time.perf_counter()
         reps = 0
         while time.perf_counter() - t0 < seconds:
+            c = reps % copies
+            sl = slice(c * len(experts), (c + 1) * len(experts))
             assert orc.orc().orc_lane_layer(18, 18, dim, ff, math.inf, orc.ptr(rows_x), orc.ptr(scale), len(pairs),
-                                            tab(mats["g"]), tab(mats["u"]), tab(mats["d"]), orc.ptr(r0), orc.ptr(cnt),
-                                            len(experts), orc.ptr(y))
+                                            tab(rot["g"][sl]), tab(rot["u"][sl]), tab(rot["d"][sl]), orc.ptr(r0),
+                                            orc.ptr(cnt), len(experts), orc.ptr(y))
             reps += 1
         per = (time.perf_counter() - t0) / reps
-    del torch
-    step_bytes = len(experts) * lay["per_expert"] + n_tok * dim * 8
+    del torch, rot
+    cold = "cold: %d weight copies rotated (%.0f MB against a %.0f MB last-level cache)" % (
+        copies, copies * step_bytes / 1e6, llc / 1e6)
     out = {"value": round(step_bytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-           "sample": "%d x one %d-token step of the same layer (%d experts' gate/up/down, int8 lane), %.2f ms a step"
-                     % (reps, n_tok, len(experts), per * 1e3)}
+           "sample": "%d x one %d-token step of the same layer (%d experts' gate/up/down, int8 lane), %.2f ms a step; %s"
+                     % (reps, n_tok, len(experts), per * 1e3, cold),
+           "llc_bytes": llc}
     if kind == "reference":
         out["one_core"] = {"value": round(step_bytes / per1 / 1e9, 3), "unit": "GB/s",
-                           "sample": "%d x the same step on one thread, %.2f ms a step" % (reps1, per1 * 1e3)}
+                           "sample": "%d x the same step on one thread, %.2f ms a step (the same rotation)"
+                                     % (reps1, per1 * 1e3)}
     return out
 
 

@@ -85,6 +85,7 @@ def ref():
         _sig(lib, "ref_q8_rows_mt", B, U32, P, U32, U32, P, P, U32, P, U32, I32)
         _sig(lib, "ref_mv_rows", B, U32, P, U32, U32, U32, P, U32, U32, P, U32)
         _sig(lib, "ref_lane_layer_mt", B, U32, U32, U32, P, P, P, P, P, U32, U32, P, P, P, P, I32, I32)
+        _sig(lib, "ref_lane_layer_rot", B, U32, U32, U32, P, P, P, P, P, U32, U32, P, P, P, P, I32, I32, U32)
         _ref = lib
     return _ref
 

@@ -82,6 +82,7 @@ struct Layer {
   float *gs, *us, *h, *hd, *y;
   int8_t *hq;
   int threads, reps;
+  uint32_t copies;  // rep r reads weight copy r % copies: tables g, u, dn hold copies x n_e matrices
   pthread_barrier_t bar;
   bool ok;
 };
@@ -102,15 +103,17 @@ static void *layer_worker(void *p)
   Layer *L = w->L;
   const uint32_t D = L->dim, F = L->ff;
   for (int rep = 0; rep < L->reps; rep++) {
+    const uint64_t cp = (uint64_t)(rep % L->copies) * L->n_e;
+    const void *const *G = L->g + cp, *const *U = L->u + cp, *const *DN = L->dn + cp;
     uint64_t a, b;
     span((uint64_t)L->n_e * F, w->id, L->threads, &a, &b);  // gate / up rows of all experts end to end
     for (uint32_t e = 0; e < L->n_e; e++) {
       const uint64_t lo = (uint64_t)e * F, r0 = a > lo ? a - lo : 0, r1 = b < lo + F ? b - lo : F;
       if (r0 >= r1 || lo >= b) continue;
       const uint64_t row = L->r0[e];
-      if (!cpu_q8_rows(L->type, L->g[e], D, (uint32_t)r0, (uint32_t)r1, L->q + row * D, L->d + row * (D / 32),
+      if (!cpu_q8_rows(L->type, G[e], D, (uint32_t)r0, (uint32_t)r1, L->q + row * D, L->d + row * (D / 32),
                        L->cnt[e], L->gs + row * F, F) ||
-          !cpu_q8_rows(L->type, L->u[e], D, (uint32_t)r0, (uint32_t)r1, L->q + row * D, L->d + row * (D / 32),
+          !cpu_q8_rows(L->type, U[e], D, (uint32_t)r0, (uint32_t)r1, L->q + row * D, L->d + row * (D / 32),
                        L->cnt[e], L->us + row * F, F))
         L->ok = false;
       for (uint32_t t = 0; t < L->cnt[e]; t++)
@@ -129,7 +132,7 @@ static void *layer_worker(void *p)
       const uint64_t lo = (uint64_t)e * D, r0 = a > lo ? a - lo : 0, r1 = b < lo + D ? b - lo : D;
       if (r0 >= r1 || lo >= b) continue;
       const uint64_t row = L->r0[e];
-      if (!cpu_q8_rows(L->type, L->dn[e], F, (uint32_t)r0, (uint32_t)r1, L->hq + row * F, L->hd + row * (F / 32),
+      if (!cpu_q8_rows(L->type, DN[e], F, (uint32_t)r0, (uint32_t)r1, L->hq + row * F, L->hd + row * (F / 32),
                        L->cnt[e], L->y + row * D, D))
         L->ok = false;
     }
@@ -138,13 +141,17 @@ static void *layer_worker(void *p)
   return nullptr;
 }
 
-bool ref_lane_layer_mt(uint32_t type, uint32_t dim, uint32_t ff, const void *const *g, const void *const *u,
-                       const void *const *dn, const uint32_t *r0, const uint32_t *cnt, uint32_t n_e, uint32_t n_rows,
-                       const int8_t *q, const float *d, const float *scale, float *y, int threads, int reps)
+// the layer `reps` times on `threads` threads, repetition r on weight copy r % copies (g, u and dn hold copies x n_e
+// matrix addresses, copy after copy): with more copies than the host's last-level cache holds, every repetition reads
+// its weights from DRAM, as a decode step does
+bool ref_lane_layer_rot(uint32_t type, uint32_t dim, uint32_t ff, const void *const *g, const void *const *u,
+                        const void *const *dn, const uint32_t *r0, const uint32_t *cnt, uint32_t n_e, uint32_t n_rows,
+                        const int8_t *q, const float *d, const float *scale, float *y, int threads, int reps,
+                        uint32_t copies)
 {
-  if (threads < 1 || threads > 256 || reps < 1) return false;
+  if (threads < 1 || threads > 256 || reps < 1 || copies < 1) return false;
   Layer L = {type, dim, ff, n_e, n_rows, g, u, dn, r0, cnt, q, d, scale, nullptr, nullptr, nullptr, nullptr, y,
-             nullptr, threads, reps, {}, true};
+             nullptr, threads, reps, copies, {}, true};
   L.gs = new float[(size_t)n_rows * ff], L.us = new float[(size_t)n_rows * ff], L.h = new float[(size_t)n_rows * ff];
   L.hd = new float[(size_t)n_rows * (ff / 32)], L.hq = new int8_t[(size_t)n_rows * ff];
   pthread_barrier_init(&L.bar, nullptr, (unsigned)threads);
@@ -155,6 +162,13 @@ bool ref_lane_layer_mt(uint32_t type, uint32_t dim, uint32_t ff, const void *con
   pthread_barrier_destroy(&L.bar);
   delete[] L.gs, delete[] L.us, delete[] L.h, delete[] L.hd, delete[] L.hq;
   return L.ok;
+}
+
+bool ref_lane_layer_mt(uint32_t type, uint32_t dim, uint32_t ff, const void *const *g, const void *const *u,
+                       const void *const *dn, const uint32_t *r0, const uint32_t *cnt, uint32_t n_e, uint32_t n_rows,
+                       const int8_t *q, const float *d, const float *scale, float *y, int threads, int reps)
+{
+  return ref_lane_layer_rot(type, dim, ff, g, u, dn, r0, cnt, n_e, n_rows, q, d, scale, y, threads, reps, 1);
 }
 
 }  // extern "C"

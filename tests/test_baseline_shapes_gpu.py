@@ -6,11 +6,12 @@ pinned oracle:
 - config 2: Q4_K and Q3_K, 2048 -> 6144 from N(0, 0.02): mv_strided at 1 / 8 / 64 tokens (oracle rows at both ends
   of the matrix), the lane at 1 and 8 tokens (every row), mm_run at 8 and 64 tokens within the reference's f16 bound;
 - config 3: the Qwen-style layer at its full expert count (512 experts, hidden 2048, expert ff 512, top-10, IQ3_XXS)
-  at batches 1 and 32;
+  at batches 1, 4 and 32;
 - config 4: the DeepSeek-style layer at its full expert count (256 routed + the shared one, hidden 7168, expert ff
-  2048, top-9) in IQ1_S and IQ1_M at batches 1 and 4;
+  2048, top-9) in IQ1_S, IQ1_M and IQ2_XXS at batches 1 and 4;
 - config 5: the benchmark's own routing (512 tokens top-8 of 256 experts, Zipf 1.1, seed 11): mmq_group over Q4_K
-  2048 -> 7168 and osmos_lane_group over IQ2_XXS 7168 -> 2048, every expert launched; the busiest expert (all of its
+  2048 -> 7168, and osmos_lane_group and mm_group (f16, the kernel form the benchmark times) over IQ2_XXS
+  7168 -> 2048, every expert launched; the busiest expert (all of its
   tokens) and two small ones checked on 64-row subsets, and tokens of the busiest expert run alone for batch
   invariance.
 (reference checks of the same kind: tests/gpu/test_q8_gpu.hip:232-244, tests/gpu/test_mmq_gpu.hip:207-233,
@@ -121,7 +122,7 @@ def test_config2_mm_bound(g, name):
     assert (g.bits(ys[8]) == g.bits(ys[64][:8])).all()
 
 
-@pytest.mark.parametrize("n_tok", [1, 32])
+@pytest.mark.parametrize("n_tok", [1, 4, 32])
 def test_config3_qwen_layer_512_experts(g, n_tok):
     """the Qwen-style layer at full size: 512 experts (each its own weights), hidden 2048, ff 512, top-10, IQ3_XXS"""
     import torch
@@ -166,12 +167,12 @@ def _device_blocks(g, name, n, seed):
     return blk
 
 
-@pytest.mark.parametrize("name", ["IQ1_S", "IQ1_M"])
+@pytest.mark.parametrize("name", ["IQ1_S", "IQ1_M", "IQ2_XXS"])
 @pytest.mark.parametrize("n_tok", [1, 4])
 def test_config4_deepseek_layer_257_experts(g, name, n_tok):
     """the DeepSeek-style layer at its full expert count: 256 routed experts plus the shared one as a ninth pick
-    (257 matrices of each kind, hidden 7168, expert ff 2048), IQ1_S and IQ1_M, batches 1 and 4 (the draft/verify
-    batch): the oracle's bits. (weights made on the device; the routed experts' copied back for the oracle)"""
+    (257 matrices of each kind, hidden 7168, expert ff 2048), IQ1_S and IQ1_M, and IQ2_XXS for comparison, batches 1
+    and 4 (the draft/verify batch): the oracle's bits. (weights made on the device; the routed experts' copied back for the oracle)"""
     import torch
     from libosmos_amd.layer import LaneLayer
     from tests.test_moe_gpu import _lane_layer_oracle
@@ -310,3 +311,53 @@ def test_config5_lane_group(g):
                g.a(g.dev(np.zeros(1, np.int32))), 1, 1, rows, cols, g.a(g.dev(q[a + j:a + j + 1])),
                g.a(g.dev(d[a + j:a + j + 1])), g.a(y1), rows, None)
         assert (g.bits(g.host(y1)[0]) == g.bits(yh[a + j])).all(), j
+
+
+def test_config5_mm_group_iq2xxs(g):
+    """mm_group at the benchmark's config-5 gate: IQ2_XXS 7168 -> 2048, 256 table entries at the Zipf routing (the
+    441-token busiest expert, so the tall row-tile form the benchmark times), within the reference's f16 bound on a
+    64-row subset for the busiest expert and two small ones, and three tokens of the busiest expert alone the same
+    bits (reference tests/gpu/test_mm_gpu.hip:321-341)"""
+    import torch
+    from tests.test_mm_gpu import bound_check
+    pairs = _cfg5_routing()
+    n_exp, n_tok, rows, cols = 256, 512, 2048, 7168
+    name = "IQ2_XXS"
+    t = synth.ID[name]
+    cnt = np.array([len(p) for p in pairs], np.int32)
+    mats = [synth.iq_blocks(t, rows, cols, 700 + m) for m in range(N_MATS)]
+    dm = [g.dev(m) for m in mats]
+    idx, soff = [], np.zeros(n_exp, np.uint32)
+    for e in range(n_exp):
+        soff[e] = len(idx)
+        idx += pairs[e] + [-1] * ((-len(pairs[e])) % 16)
+    slots = len(idx)
+    x = synth.normal((n_tok, cols), 15)
+    xd = g.dev(x)
+    x16 = torch.zeros(slots * cols, dtype=torch.float16, device="cuda")
+    g.call("mm_x16_rows", g.a(xd), cols, g.a(g.dev(np.array(idx, np.int32))), slots, cols, g.a(x16), None, None)
+    xoff = (soff.astype(np.int64) * cols).astype(np.uint32)
+    yoff = (soff.astype(np.int64) * rows).astype(np.uint32)
+    y = torch.full((slots * rows,), float("nan"), device="cuda")
+    print("config 5 mm_group IQ2_XXS", flush=True)
+    g.call("mm_group", t, g.a(g.table([dm[e % N_MATS] for e in range(n_exp)])), g.a(g.dev(cnt)), n_exp,
+           int(cnt.max()), rows, cols, g.a(x16), g.a(g.dev(xoff)), cols, g.a(y), g.a(g.dev(yoff)), rows, None)
+    yh = g.host(y).reshape(slots, rows)
+    live = np.array([i >= 0 for i in idx])
+    assert np.isfinite(yh[live]).all()
+    busiest, small = _checked_experts(pairs)
+    assert len(pairs[busiest]) == 441
+    r0, r1 = 1000, 1064
+    for e in [busiest] + small:
+        a, c = int(soff[e]), len(pairs[e])
+        bound_check(name, np.ascontiguousarray(mats[e % N_MATS][r0:r1]), r1 - r0, cols, x[pairs[e]],
+                    yh[a:a + c, r0:r1])
+    for j in (0, 200, 440):
+        tok = pairs[busiest][j]
+        x1 = torch.zeros(16 * cols, dtype=torch.float16, device="cuda")
+        g.call("mm_x16_rows", g.a(xd), cols, g.a(g.dev(np.array([tok], np.int32))), 1, cols, g.a(x1), None, None)
+        y1 = torch.full((rows,), float("nan"), device="cuda")
+        z = g.dev(np.zeros(1, np.uint32))
+        g.call("mm_group", t, g.a(g.table([dm[busiest % N_MATS]])), g.a(g.dev(np.array([1], np.int32))), 1, 1, rows,
+               cols, g.a(x1), g.a(z), cols, g.a(y1), g.a(z), rows, None)
+        assert (g.bits(g.host(y1)) == g.bits(yh[int(soff[busiest]) + j])).all(), j
