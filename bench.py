@@ -447,15 +447,6 @@ def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=
             graphs.append((graph, n))
         else:
             graphs.append(graphs[0])
-    # the runtime's graph path warmed once before the timed region: the process's first graph replay pays a one-time
-    # setup (about 12 us a 20-step region, measured), which belongs to the runtime, not to the steps. A graph of one
-    # zero fill - no layer work - replayed once
-    warm = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(warm, stream=s):
-            add.zero_()
-    torch.cuda.synchronize()
-    warm.replay()
     torch.cuda.synchronize()
     ev = Events(torch)
     ms = ev.time(lambda: [g.replay() for g, _ in graphs], 1)
