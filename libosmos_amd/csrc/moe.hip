@@ -27,12 +27,14 @@ constexpr uint32_t kMaxExperts = 1024, kMaxK = 32;
 constexpr float kSumFloor = 6.103515625e-5f;
 constexpr int kTile = 16, kPart = kTile << (Q4X_TILE_RUNS - 1);  // 128: an entry's most tokens
 
-__device__ inline float pick_key(float x) { return x == x ? x : -__builtin_inff(); }
 __device__ inline float sigmoid(float x) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x))); }
 __device__ inline float silu(float x) { return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x))); }  // (kernels/block.h:87)
 
-// ---- q4x_route: a workgroup a token; the softmax by workgroup trees, the picks by its first wave ----
-constexpr int kRouteThreads = 256, kRouteLane = kMaxExperts / kWave;
+// ---- q4x_route: a workgroup a token. the softmax by workgroup trees; the picks by a sort: each expert becomes one
+// 64-bit key (its probability's order-preserving bits above, its id inverted below, so a greater probability and then
+// a lower id sort first; NaN ranks as -inf, below every number), the token's keys are sorted descending by a bitonic
+// network in LDS, and the first k are the picks in order ----
+constexpr int kRouteThreads = 512;
 
 __device__ inline float wg_reduce(float v, float* lds, bool is_max) {
   lds[threadIdx.x] = v;
@@ -47,10 +49,22 @@ __device__ inline float wg_reduce(float v, float* lds, bool is_max) {
   return r;
 }
 
+// the sort key of expert e with probability p (a softmax output: +0 .. 1, or NaN); 0 for a slot past the experts
+__device__ inline uint64_t route_key(float p, uint32_t e, uint32_t n_exp) {
+  if (e >= n_exp) return 0;
+  const uint32_t rank = p == p ? (__float_as_uint(p) & 0x7FFFFFFFu) + 1u : 0u;  // (NaN: -inf's rank, under +0's)
+  return (uint64_t) rank << 32 | (0xFFFFFFFFu - e);
+}
+__device__ inline float key_value(uint64_t key) {  // the pick's probability as the weights take it (NaN: -inf)
+  const uint32_t rank = (uint32_t) (key >> 32);
+  return rank ? __uint_as_float(rank - 1u) : -__builtin_inff();
+}
+
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* __restrict__ logits, uint32_t n_exp,
                                                               uint32_t k, int32_t* __restrict__ ids,
                                                               float* __restrict__ w, int32_t* __restrict__ rows) {
   __shared__ float p[kMaxExperts], lds[kRouteThreads];
+  __shared__ uint64_t key[kMaxExperts];
   const uint32_t t = blockIdx.x;
   const float* l = logits + (uint64_t) t * n_exp;
   float m = -__builtin_inff();
@@ -59,33 +73,33 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(const float* __res
   float sum = 0.0f;
   for (uint32_t i = threadIdx.x; i < n_exp; i += kRouteThreads) sum = __fadd_rn(sum, (p[i] = expf(__fsub_rn(l[i], m))));
   const float inv = __fdiv_rn(1.0f, wg_reduce(sum, lds, false));
-  for (uint32_t i = threadIdx.x; i < n_exp; i += kRouteThreads) p[i] = __fmul_rn(p[i], inv);
+  for (uint32_t i = threadIdx.x; i < kMaxExperts; i += kRouteThreads)
+    key[i] = route_key(i < n_exp ? __fmul_rn(p[i], inv) : 0.0f, i, n_exp);
   __syncthreads();
-  if (threadIdx.x >= kWave) return;
-  const uint32_t lane = threadIdx.x;
-  float v[kRouteLane];
-  for (int r = 0; r < kRouteLane; r++) v[r] = lane + kWave * r < n_exp ? pick_key(p[lane + kWave * r]) : -__builtin_inff();
-  uint32_t taken = 0;
-  float pick[kMaxK], total = 0.0f;
-  for (uint32_t j = 0; j < k; j++) {
-    float bv = -__builtin_inff();
-    int bi = INT32_MAX;
-    for (int r = 0; r < kRouteLane; r++) {  // ascending ids within the lane: a strict > keeps the lowest
-      const uint32_t e = lane + kWave * r;
-      if (e < n_exp && !(taken >> r & 1) && (bi == INT32_MAX || v[r] > bv)) bv = v[r], bi = (int) e;
+  // bitonic sort, descending, over the smallest power of two holding the experts: stage (size, dist) compares i with
+  // i ^ dist, the pair's order descending where bit `size` of i is clear
+  uint32_t n2 = 1;
+  while (n2 < n_exp) n2 <<= 1;
+  for (uint32_t size = 2; size <= n2; size <<= 1)
+    for (uint32_t dist = size >> 1; dist > 0; dist >>= 1) {
+      for (uint32_t i = threadIdx.x; i < n2; i += kRouteThreads) {
+        const uint32_t j = i ^ dist;
+        if (j > i) {
+          const uint64_t a = key[i], b = key[j];
+          const bool down = (i & size) == 0;
+          if (down ? a < b : a > b) key[i] = b, key[j] = a;
+        }
+      }
+      __syncthreads();
     }
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, kWave);
-      const int oi = __shfl_xor(bi, o, kWave);
-      if (oi != INT32_MAX && (bi == INT32_MAX || ov > bv || (ov == bv && oi < bi))) bv = ov, bi = oi;
-    }
-    if ((uint32_t) bi % kWave == lane) taken |= 1u << ((uint32_t) bi / kWave);
-    pick[j] = bv, total = __fadd_rn(total, bv);
-    if (!lane) ids[t * k + j] = bi, rows[t * k + j] = (int32_t) t;
+  if (threadIdx.x == 0) {  // the picks in order, their weights over max(their sum, the floor)
+    float total = 0.0f;
+    for (uint32_t j = 0; j < k; j++) total = __fadd_rn(total, key_value(key[j]));
+    const float div = fmaxf(total, kSumFloor);
+    for (uint32_t j = 0; j < k; j++) w[t * k + j] = __fdiv_rn(key_value(key[j]), div);
   }
-  if (lane) return;
-  const float div = fmaxf(total, kSumFloor);
-  for (uint32_t j = 0; j < k; j++) w[t * k + j] = __fdiv_rn(pick[j], div);
+  for (uint32_t j = threadIdx.x; j < k; j += kRouteThreads)
+    ids[t * k + j] = (int32_t) (0xFFFFFFFFu - (uint32_t) key[j]), rows[t * k + j] = (int32_t) t;
 }
 
 // ---- q4x_expert_tiles ----

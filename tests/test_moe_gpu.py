@@ -44,6 +44,30 @@ def test_route(g):
         assert (g.host(rows) == np.repeat(np.arange(n_tok), k)).all()
 
 
+def test_route_ties_and_zeros(g):
+    """all logits equal (every probability the same: the k lowest ids in order), and fewer finite logits than k (the
+    rest of the picks are the zero-probability experts, lowest ids first), against the oracle's ids and weights"""
+    import torch
+    n_exp, k = 64, 8
+    logits = np.zeros((3, n_exp), np.float32)
+    logits[1, :] = -np.inf
+    logits[1, [40, 3, 17, 60, 9]] = [1.0, 0.5, 1.0, -2.0, 0.25]
+    logits[2, :] = np.linspace(-3, 3, n_exp).astype(np.float32)[::-1]
+    n_tok = logits.shape[0]
+    ids = torch.zeros(n_tok * k, dtype=torch.int32, device="cuda")
+    w = torch.zeros(n_tok * k, dtype=torch.float32, device="cuda")
+    rows = torch.zeros(n_tok * k, dtype=torch.int32, device="cuda")
+    g.call("q4x_route", g.a(g.dev(logits)), n_tok, n_exp, k, g.a(ids), g.a(w), g.a(rows), None)
+    oi = np.zeros(n_tok * k, np.int32)
+    ow = np.zeros(n_tok * k, np.float32)
+    orc.orc().orc_route(orc.ptr(logits), n_tok, n_exp, k, orc.ptr(oi), orc.ptr(ow))
+    gi = g.host(ids)
+    assert (gi == oi).all()
+    assert (gi[:k] == np.arange(k)).all()
+    assert (gi[k:k + 5] == [17, 40, 3, 9, 60]).all() and (gi[k + 5:2 * k] == [0, 1, 2]).all()
+    assert np.allclose(g.host(w), ow, rtol=1e-6, atol=0)
+
+
 def tiles_ref(ids, k, n_exp, dim, ff, bases, nbytes):
     """q4x_expert_tiles' contract restated on the host (a stable sort by expert)"""
     n = len(ids)
