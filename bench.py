@@ -442,8 +442,8 @@ def moe_layer_bench(torch, capi, n_tok, steps, warmup, rotate_bytes=2.2e9, seed=
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.stream(s):
                 with torch.cuda.graph(graph, stream=s):
-                    for st in range(n):
-                        run(st)
+                    for st in range(n):  # (steps after the warmup's: no timed step repeats a warmup step's experts)
+                        run(warmup + st)
             graphs.append((graph, n))
         else:
             graphs.append(graphs[0])

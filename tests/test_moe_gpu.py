@@ -106,8 +106,12 @@ def test_expert_tiles(g):
     rng = np.random.default_rng(2)
     cases = [(3, 10, 512, False), (512, 8, 256, False), (40, 4, 64, True), (100, 8, 256, False), (128, 8, 256, True),
              (129, 8, 256, False), (300, 10, 1024, True), (1, 1, 1, False)]
+    for _ in range(12):  # random shapes: expert counts off the powers of two, k up to 32, both placement paths
+        n_exp = int(rng.integers(1, 1025))
+        k = int(rng.integers(1, min(32, n_exp) + 1))
+        cases.append((int(rng.integers(1, 2600 // k + 1)), k, n_exp, bool(rng.integers(0, 2))))
     for n_tok, k, n_exp, use_tab in cases:
-        if n_tok >= 128:  # Zipf(1.1) load skew, distinct experts a token
+        if n_tok >= 128 and n_exp >= 8 * k:  # Zipf(1.1) load skew, distinct experts a token
             p = 1.0 / np.arange(1, n_exp + 1) ** 1.1
             p /= p.sum()
             ids = np.concatenate([rng.choice(n_exp, k, replace=False, p=p) for _ in range(n_tok)]).astype(np.int32)
