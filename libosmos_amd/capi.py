@@ -35,6 +35,8 @@ SIGS = {
     "q4x_expert_tiles": (B, [P, U32, U32, U32, U32, U32, P, P]),
     "q4x_moe_sum": (B, [P, P, P, U32, U32, U32, P, P, P, P]),
     "q4x_swiglu_rows": (B, [P, P, U32, P, U32, P, P, P]),
+    "q4x_swiglu": (B, [P, P, U64, P, P, P]),
+    "q4x_spin": (B, [U32, P]),
     "ops_wait": (B, [P, U32, P]),
     "osmos_wait_limit": (None, [U64]),
     "ops_copy_rows": (B, [P, P, P, U32, U32, P]),
@@ -65,6 +67,11 @@ class Q4xExpertTiles(ctypes.Structure):
     """include/osmos/gpu/q4x_ops.h's Q4xExpertTiles"""
     _fields_ = [("base", P * 3), ("bytes", U64 * 3), ("tab", P * 3), ("ptr", P * 3), ("cnt", P), ("gidx", P),
                 ("hidx", P), ("xg", P), ("yg", P), ("xd", P), ("yd", P), ("where", P), ("off", P)]
+
+
+class Q4xX16(ctypes.Structure):
+    """include/osmos/gpu/q4x_ops.h's Q4xX16"""
+    _fields_ = [("x16", P), ("overflow", P), ("cols", U32), ("row0", U32)]
 
 
 class Q4xExpertBounds(ctypes.Structure):

@@ -284,6 +284,33 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ 
   out[i] = __fadd_rn(sum, __fmul_rn(shared[i], sigmoid(shared_logit[t])));
 }
 
+// ---- q4x_swiglu (kernels/q4x_moe.hip:167-170): a thread 4 values, each silu(g) u (swiglu_rows_kernel's expression),
+// and, with a side output, its f16 at its (row, column) of the tiled x16 ----
+struct Side {
+  _Float16* x16;
+  int32_t* overflow;
+  uint32_t cols, row0;
+};
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* g, const float* u, uint64_t n, float* y, Side side) {
+  const uint64_t i0 = ((uint64_t) blockIdx.x * 256 + threadIdx.x) * 4;
+  bool over = false;
+#pragma unroll
+  for (uint64_t i = i0; i < i0 + 4; i++) {
+    if (i >= n) break;
+    const float v = __fmul_rn(silu(g[i]), u[i]);
+    y[i] = v;
+    if (side.x16) side.x16[x16_at(side.row0 + (uint32_t) (i / side.cols), (uint32_t) (i % side.cols), side.cols)] = x16_round(v, over);
+  }
+  if (over) *side.overflow = 1;
+}
+
+// ---- q4x_spin: one thread sleeping until the constant-rate clock has moved on by `ticks` ----
+__global__ __launch_bounds__(64) void spin_kernel(uint64_t ticks) {
+  if (threadIdx.x) return;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
 // ---- ops ----
 __global__ __launch_bounds__(256) void swiglu_lane_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                                           uint32_t n, float lim, const float* __restrict__ scale,
@@ -474,6 +501,25 @@ extern "C" OSM_API bool q4x_expert_tiles(const int32_t* ids, uint32_t n, uint32_
   moe::tiles_kernel<<<1, moe::kTileThreads, 0, s>>>(ids, n, k, n_exp, dim, ff, *t, bd);
   if (hipGetLastError() != hipSuccess) return false;
   if (n > moe::kPlaceInline) moe::place_kernel<<<n_exp, moe::kPlaceThreads, 0, s>>>(ids, n, k, n_exp, *t);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool q4x_swiglu(const float* g, const float* u, uint64_t n, float* y, const Q4xX16* side,
+                                   void* stream) {
+  if (!g || !u || !y || !n) return false;
+  moe::Side sd{nullptr, nullptr, 1, 0};
+  if (side && side->x16) {
+    if (!side->overflow || !side->cols) return false;
+    sd = moe::Side{(_Float16*) side->x16, side->overflow, side->cols, side->row0};
+  }
+  const uint64_t threads = (n + 3) / 4;
+  if ((threads + 255) / 256 > 0x7FFFFFFFull) return false;
+  moe::swiglu_kernel<<<(uint32_t) ((threads + 255) / 256), 256, 0, (hipStream_t) stream>>>(g, u, n, y, sd);
+  return hipGetLastError() == hipSuccess;
+}
+
+extern "C" OSM_API bool q4x_spin(uint32_t us, void* stream) {
+  moe::spin_kernel<<<1, 64, 0, (hipStream_t) stream>>>((uint64_t) us * 100ull);  // (s_memrealtime: 100 MHz)
   return hipGetLastError() == hipSuccess;
 }
 

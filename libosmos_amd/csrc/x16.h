@@ -13,11 +13,12 @@ __host__ __device__ inline uint64_t x16_at(uint32_t t, uint32_t c, uint32_t xts)
   return (uint64_t) (t / kX16Tile) * kX16Tile * xts + (c / 16) * 256 + (t % kX16Tile) * 16 + c % 16;
 }
 
-// a value's f16 (nearest, ties to even) and whether it left f16's range (or was not a number)
+// a value's f16 (nearest, ties to even) and whether the value is past f16's largest finite, 65504, or not a number
+// (the reference's overflow rule, kernels/mm.h:47-50: the value itself, before rounding - 65510 is flagged though it
+// rounds to 65504)
 __device__ inline _Float16 x16_round(float v, bool& over) {
-  const _Float16 h = (_Float16) v;
-  over |= !(__builtin_fabsf((float) h) <= 65504.0f);
-  return h;
+  over |= !(__builtin_fabsf(v) <= 65504.0f);
+  return (_Float16) v;
 }
 
 }  // namespace osm

@@ -268,3 +268,89 @@ def test_mm_partition_order(g, name, cols, group):
     else:
         got = run(g, name, w, 16, cols, x16, n)
     assert (g.bits(got) == g.bits(want)).all()
+
+
+def test_swiglu_side_and_rows_agree(g):
+    """q4x_swiglu's F32 output within an ulp-level bound of float64 SiLU (exp is the device library's: parity
+    unpinned to the bit); its f16 side copy byte for byte mm_x16's of that output; and q4x_swiglu_rows on the same
+    rows the same bytes as q4x_swiglu then mm_x16_rows (the reference's own check, tests/gpu/test_q4x_moe_gpu.hip:117-
+    130); in place (y = g) the same values"""
+    import ctypes
+    import torch
+    from libosmos_amd import capi
+    rng = np.random.default_rng(21)
+    rows_, ff = 37, 96
+    gg = rng.normal(0, 3, (rows_, ff)).astype(np.float32)
+    uu = rng.normal(0, 3, (rows_, ff)).astype(np.float32)
+    n = rows_ * ff
+    y = torch.full((rows_, ff), float("nan"), device="cuda")
+    x16 = torch.full((48 * ff,), float("nan"), dtype=torch.float16, device="cuda")
+    ov = torch.zeros(1, dtype=torch.int32, device="cuda")
+    side = capi.Q4xX16(x16.data_ptr(), ov.data_ptr(), ff, 3)  # rows 3 .. 39 of the tiled x16
+    gd, ud = g.dev(gg), g.dev(uu)
+    g.call("q4x_swiglu", g.a(gd), g.a(ud), n, g.a(y), ctypes.byref(side), None)
+    yh = g.host(y)
+    ref = gg.astype(np.float64) / (1.0 + np.exp(-gg.astype(np.float64))) * uu.astype(np.float64)
+    assert (np.abs(yh - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-30).all()
+    # the side copy: mm_x16 of y, placed at rows 3 ..
+    want16 = torch.zeros(48 * ff, dtype=torch.float16, device="cuda")
+    ov2 = torch.zeros(1, dtype=torch.int32, device="cuda")
+    padded = np.zeros((40, ff), np.float32)
+    padded[3:] = yh
+    g.call("mm_x16", g.a(g.dev(padded)), ff, 40, ff, g.a(want16), g.a(ov2), None)
+    got16 = g.host(x16).reshape(-1).view(np.uint16)
+    w16 = g.host(want16).reshape(-1).view(np.uint16)
+    live = np.zeros((48, ff), np.float32)
+    live[3:40] = 1.0
+    lv = x16_layout(live, 48).astype(bool)
+    assert (got16[lv] == w16[lv]).all()
+    assert np.isnan(g.host(x16).reshape(-1)[~lv]).all()
+    assert int(g.host(ov)[0]) == 0
+    # q4x_swiglu_rows over the same rows = q4x_swiglu then mm_x16_rows, byte for byte
+    idx = np.array([5, -1, 0, 36, 5, 17], np.int32)
+    r16 = torch.zeros(16 * ff, dtype=torch.float16, device="cuda")
+    g.call("q4x_swiglu_rows", g.a(gd), g.a(ud), ff, g.a(g.dev(idx)), len(idx), g.a(r16), g.a(ov), None)
+    m16 = torch.zeros(16 * ff, dtype=torch.float16, device="cuda")
+    g.call("mm_x16_rows", g.a(y), ff, g.a(g.dev(idx)), len(idx), ff, g.a(m16), g.a(ov2), None)
+    assert (g.host(r16).view(np.uint16) == g.host(m16).view(np.uint16)).all()
+    # in place
+    g.call("q4x_swiglu", g.a(gd), g.a(ud), n, g.a(gd), None, None)
+    assert (g.bits(g.host(gd)) == g.bits(yh)).all()
+
+
+def test_f16_overflow_rule():
+    """the side copies' and mm_x16's overflow flag is the reference's rule (kernels/mm.h:47-50): a value past 65504 or
+    not a number, judged before rounding - 65510 rounds to 65504 and is still flagged; 65504 itself is not"""
+    import ctypes
+    import torch
+    from libosmos_amd import capi
+    from tests import gpu_util as g
+    ff = 16
+    for v, flagged in ((65504.0, False), (65510.0, True), (-70000.0, True), (float("nan"), True), (1.0, False)):
+        x = np.ones((1, ff), np.float32)
+        x[0, 5] = v
+        x16 = torch.zeros(16 * ff, dtype=torch.float16, device="cuda")
+        ov = torch.zeros(1, dtype=torch.int32, device="cuda")
+        g.call("mm_x16", g.a(g.dev(x)), ff, 1, ff, g.a(x16), g.a(ov), None)
+        assert bool(g.host(ov)[0]) == flagged, v
+        ov.zero_()
+        side = capi.Q4xX16(x16.data_ptr(), ov.data_ptr(), ff, 0)
+        one = g.dev(np.full((1, ff), 1e30, np.float32))  # silu(1e30) = 1e30: u = v / 1e30 gives y = v
+        uu = g.dev((x / np.float32(1e30)).astype(np.float32))
+        y = torch.zeros(1, ff, device="cuda")
+        g.call("q4x_swiglu", g.a(one), g.a(uu), ff, g.a(y), ctypes.byref(side), None)
+        if np.isfinite(v):
+            assert bool(g.host(ov)[0]) == (abs(float(g.host(y)[0, 5])) > 65504.0), v
+
+
+def test_spin_holds_the_stream():
+    """q4x_spin holds its stream for at least the asked time (events around it), and refuses nothing"""
+    import torch
+    from tests import gpu_util as g
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    g.call("q4x_spin", 2000, None)
+    b.record()
+    torch.cuda.synchronize()
+    assert a.elapsed_time(b) >= 1.9
