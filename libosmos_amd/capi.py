@@ -52,6 +52,8 @@ SIGS = {
     "ops_gather_sum_add": (B, [P, P, P, U32, U32, U32, P, P]),
     "osmos_lane_tables": (B, [P, U32, U32, U32, P, P, P, P, P, P, P, P, P, P, P]),
     "quant_dequant": (B, [U32, P, U64, P, P]),
+    "quant_dequant_f16": (B, [U32, P, U64, P, P]),
+    "quant_repack_q5k": (B, [P, U32, U32, P, P]),
 }
 
 
@@ -87,6 +89,16 @@ SIGS.update({
     "osmos_lane_group": (B, [U32, P, P, P, U32, U32, U32, U32, P, P, P, U32, P]),
 })
 
+
+
+# include/osmos/gpu/quant.h
+QUANT_Q5_K = 13
+QUANT_Q5_KR = 0x100 | QUANT_Q5_K
+QUANT_Q5_KR_BYTES_A_BLOCK = 180
+
+
+def quant_q5kr_bytes(rows, cols):
+    return rows * (cols // 256) * QUANT_Q5_KR_BYTES_A_BLOCK
 
 
 # include/osmos/model/gguf.h (host memory: the GGUF reader touches no GPU)

@@ -20,6 +20,7 @@ constexpr int kWave = 64;  // CDNA: a wavefront is 64 lanes
 enum Type : uint32_t {
   kF32 = 0, kQ4_0 = 2, kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ2_XXS = 16,
   kIQ2_XS = 17, kIQ3_XXS = 18, kIQ1_S = 19, kIQ4_NL = 20, kIQ2_S = 22, kIQ4_XS = 23, kIQ1_M = 29, kBF16 = 30,
+  kQ5_KR = 0x100 | 13,  // Q5_K repacked in tiles of 16 rows (reference include/osmos/gpu/quant.h:17: QUANT_Q5_KR)
 };
 
 template <uint32_t T> struct Block;
@@ -34,6 +35,7 @@ OSM_BLOCK(kQ2_K, 256, 84)
 OSM_BLOCK(kQ3_K, 256, 110)
 OSM_BLOCK(kQ4_K, 256, 144)
 OSM_BLOCK(kQ5_K, 256, 176)
+OSM_BLOCK(kQ5_KR, 256, 180)  // (a row's share of its tile's block: 16 rows x 180 bytes a block of 256 columns)
 OSM_BLOCK(kQ6_K, 256, 210)
 OSM_BLOCK(kIQ2_XXS, 256, 66)
 OSM_BLOCK(kIQ2_XS, 256, 74)

@@ -59,6 +59,7 @@ OSM_CODEC(kQ3_K, 3, true, Form::kPlain)     // q2 + 4 hbit - 4 as ((q2 | hbit <<
 OSM_CODEC(kQ2_K, 2, false, Form::kMin)
 OSM_CODEC(kQ4_K, 4, false, Form::kMin)
 OSM_CODEC(kQ5_K, 5, false, Form::kMin)
+OSM_CODEC(kQ5_KR, 5, false, Form::kMin)
 OSM_CODEC(kIQ2_XXS, 8, true, Form::kPlain)
 OSM_CODEC(kIQ2_XS, 8, true, Form::kPlain)
 OSM_CODEC(kIQ2_S, 8, true, Form::kPlain)
@@ -191,6 +192,28 @@ template <> struct Layout<kQ5_K> {
     return c;
   }
 };
+// Q5_KR, Q5_K repacked (the reference's layout, include/osmos/gpu/quant.h:17-19,42-47, kernels/quant.h:117-123): rows
+// in tiles of 16; a tile's block of 256 columns is 2880 bytes - the 16 rows' f16 d and dmin (4 bytes a row), then for
+// each 32-value group g a 352-byte segment: 32 slots of 16 values (slot h 16 + r: row r's chunks 4 g + h and
+// 4 g + 2 + h) as 8 bytes of low nibbles (value i at nibble i) at slot 8, their fifth bits as 2 bytes at
+// 256 + slot 2, then each row's 6-bit scale and minimum as 2 bytes at 320 + r 2. `b` is the tile's block and chunk k
+// is r 32 + c (row r's chunk c): the same fields as Q5_K's, so the same values
+template <> struct Layout<kQ5_KR> {
+  static constexpr int kRows = 16, kHead = 64, kSeg = 352, kHighs = 256, kScales = 320;
+  template <typename Tab> __device__ static Chunk at(const Tab&, const uint8_t* b, int k) {
+    const int r = k >> 5, c = k & 31, g = c >> 2, h = c & 1, upper = (c >> 1) & 1, slot = h * kRows + r;
+    const uint8_t* seg = b + kHead + g * kSeg;
+    const uint32_t nib = ld32(seg + slot * 8 + 4 * upper);             // this chunk's 8 nibbles
+    const uint32_t hi = (ld16(seg + kHighs + slot * 2) >> (8 * upper)) & 0xFFu;  // and their fifth bits
+    const uint32_t sm = ld16(seg + kScales + r * 2);
+    // nibble i to byte i % 4 of word i / 4: spread each 16-bit half's 4 nibbles over 4 bytes
+    auto spread = [](uint32_t x) { x = (x | x << 8) & 0x00FF00FFu; return (x | x << 4) & 0x0F0F0F0Fu; };
+    // fifth bit i to bit 4 of byte i % 4 of word i / 4
+    auto highs = [](uint32_t x) { return ((x & 0xFu) * 0x00204081u & kEach) << 4; };
+    return Chunk{{spread(nib & 0xFFFFu) | highs(hi), spread(nib >> 16) | highs(hi >> 4)},
+                 mul(half_at(b + 4 * r), (float) (sm & 0xFFu)), mul(half_at(b + 4 * r + 2), (float) (sm >> 8))};
+  }
+};
 // Q6_K: 128 bytes of low nibbles, 64 bytes of 2-bit highs, 16 int8 scales (one a 16 values), f16 d. Values are in
 // halves of 128: value 128 h + 32 r + l (r < 4, l < 32) has its low nibble in byte 64 h + 32 (r & 1) + l (high nibble
 // for r >= 2) and its high pair at bits 2r of byte 128 + 32 h + l
@@ -321,6 +344,22 @@ __device__ inline const uint8_t* chunk_at(const uint8_t* row, uint32_t c, int* k
   constexpr uint32_t per = Block<T>::values / kChunk;
   *k = (int) (c % per);
   return row + (uint64_t) (c / per) * Block<T>::bytes;
+}
+// the same for any type with the row's index: its base (the row's start; Q5_KR's, its tile's) and, from it, the chunk
+// (Q5_KR: the tile's block, chunk (row % 16) 32 + c % 32)
+template <uint32_t T>
+__device__ inline const uint8_t* row_base(const uint8_t* w, uint32_t row, uint32_t cols) {
+  if constexpr (T == kQ5_KR) return w + (uint64_t) (row / 16) * 16 * row_bytes<T>(cols);
+  else return w + (uint64_t) row * row_bytes<T>(cols);
+}
+template <uint32_t T>
+__device__ inline const uint8_t* chunk_of(const uint8_t* base, uint32_t row, uint32_t c, int* k) {
+  if constexpr (T == kQ5_KR) {
+    *k = (int) ((row % 16) * 32 + c % 32);
+    return base + (uint64_t) (c / 32) * 16 * Block<T>::bytes;
+  } else {
+    return chunk_at<T>(base, c, k);
+  }
 }
 
 }  // namespace osm

@@ -168,7 +168,7 @@ struct KSplit {
 };
 template <uint32_t T> constexpr KSplit tuned() {
   switch (T) {
-    case kQ5_K: return {32, 8};
+    case kQ5_K: case kQ5_KR: return {32, 8};  // (Q5_KR: Q5_K's, a round one block - one 2880-byte piece a tile)
     case kQ4_K: return {32, 16};
     case kIQ1_M: case kIQ1_S: case kIQ2_XXS: case kIQ2_XS: case kIQ2_S: return {128, 4};
     case kIQ4_NL: case kIQ4_XS: case kQ4_0: return {64, 4};
@@ -222,22 +222,33 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
   const int tiles = (int) ((n - t0 + kTile - 1) / kTile) < CT ? (int) ((n - t0 + kTile - 1) / kTile) : CT;
   const uint32_t rb = (uint32_t) row_bytes<T>(a.cols);
   // this thread's staged words: word i of a round is row i / kWr's word i % kWr, at a 32-bit offset from the matrix
-  // (rows past the matrix: its last, staged and not stored)
+  // (rows past the matrix: its last, staged and not stored). Q5_KR: a round is one block, its tile's 16 rows' 2880
+  // bytes side by side in the matrix - word i is tile i / kWt's word i % kWt, and a tile's rows lie in LDS as there
+  constexpr bool kTiled = T == kQ5_KR;
+  static_assert(!kTiled || kRv == Block<T>::values, "a Q5_KR round one block");
+  constexpr uint32_t kWt = kTile * kRb / WB;
   uint32_t woff[kPer];
 #pragma unroll
   for (uint32_t u = 0; u < kPer; u++) {
     const uint32_t i = min(u * kThreads + threadIdx.x, kWords - 1);
-    woff[u] = min(row0 + i / kWr, a.rows - 1) * rb + (i % kWr) * WB;
+    if constexpr (kTiled) woff[u] = min(row0 / kTile + i / kWt, a.rows / kTile - 1) * kTile * rb + (i % kWt) * WB;
+    else woff[u] = min(row0 + i / kWr, a.rows - 1) * rb + (i % kWr) * WB;
   }
   word wr[kPer];
   const uint32_t nr = (a.cols + kRv - 1) / kRv;  // rounds (the last may be short: its missing slabs skipped)
   auto load = [&](uint32_t r) __attribute__((always_inline)) {
-    const uint32_t lim = (a.cols - r * kRv) / Block<T>::values * Block<T>::bytes;  // the round's bytes a row
-    const uint8_t* base = w + (uint64_t) r * kRb;
+    if constexpr (kTiled) {  // (every round whole: cols a multiple of the block)
+      const uint8_t* base = w + (uint64_t) r * kTile * kRb;
 #pragma unroll
-    for (uint32_t u = 0; u < kPer; u++) {
-      const uint32_t o = (u * kThreads + threadIdx.x) % kWr * WB;
-      wr[u] = *(const word*) (base + woff[u] - (o < lim ? 0 : o - (lim - WB)));  // (past a short round: its last word)
+      for (uint32_t u = 0; u < kPer; u++) wr[u] = *(const word*) (base + woff[u]);
+    } else {
+      const uint32_t lim = (a.cols - r * kRv) / Block<T>::values * Block<T>::bytes;  // the round's bytes a row
+      const uint8_t* base = w + (uint64_t) r * kRb;
+#pragma unroll
+      for (uint32_t u = 0; u < kPer; u++) {
+        const uint32_t o = (u * kThreads + threadIdx.x) % kWr * WB;
+        wr[u] = *(const word*) (base + woff[u] - (o < lim ? 0 : o - (lim - WB)));  // (past a short round: its last word)
+      }
     }
   };
   auto store = [&](int buf) __attribute__((always_inline)) {
@@ -267,9 +278,12 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
         half8 av[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
-          const uint8_t* row = smem + buf * kRows * kRb + (rt * kTile + lane % 16) * kRb;
           int k;
-          const uint8_t* b = chunk_at<T>(row, (wave * SL + k0) / kChunk + q, &k);
+          const uint8_t* b;
+          if constexpr (kTiled)  // (the tile's block, row lane % 16's chunk in it)
+            b = chunk_of<T>(smem + buf * kRows * kRb + rt * kTile * kRb, lane % 16, (wave * SL + k0) / kChunk + q, &k);
+          else
+            b = chunk_at<T>(smem + buf * kRows * kRb + (rt * kTile + lane % 16) * kRb, (wave * SL + k0) / kChunk + q, &k);
           if constexpr (half_path<T>()) {
             av[rt] = decode_h<T>(tab, b, k);
           } else {
@@ -424,7 +438,7 @@ bool run_by(const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
 
 #define OSM_MM_TYPES(X) \
   X(kQ8_0) X(kQ4_0) X(kIQ4_NL) X(kQ2_K) X(kQ3_K) X(kQ4_K) X(kQ5_K) X(kQ6_K) X(kIQ2_XXS) X(kIQ2_XS) X(kIQ2_S) \
-  X(kIQ3_XXS) X(kIQ1_S) X(kIQ1_M) X(kIQ4_XS)
+  X(kIQ3_XXS) X(kIQ1_S) X(kIQ1_M) X(kIQ4_XS) X(kQ5_KR)
 
 bool run(uint32_t type, const Args& a, uint32_t n_mat, uint32_t max_n, hipStream_t s) {
   switch (type) {

@@ -48,8 +48,9 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
   if (!SW && row0 >= rows) return;  // the whole half-wave: its tree's partners are its own
   const uint8_t* base[R];
 #pragma unroll
-  for (int q = 0; q < R; q++) base[q] = w + (uint64_t) (row0 + q < rows ? row0 + q : 0) * row_bytes<T>(cols);
+  for (int q = 0; q < R; q++) base[q] = row_base<T>(w, row0 + q < rows ? row0 + q : 0, cols);
   if constexpr (STG) {
+    static_assert(T != kQ5_KR, "a Q5_KR row is not contiguous");
     static_assert(R == 1, "a staged half-wave holds one row");
     __shared__ __attribute__((aligned(16))) uint8_t stg[2 * kWaves][kStgMax];
     uint8_t* slot = stg[threadIdx.x / kHalf];
@@ -83,7 +84,7 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
 #pragma unroll
     for (int q = 0; q < R; q++) {
       int k;
-      const uint8_t* b = chunk_at<T>(base[q], c, &k);
+      const uint8_t* b = chunk_of<T>(base[q], row0 + q < rows ? row0 + q : 0, c, &k);
       decode<T>(kDec, b, k, v[q]);
     }
     float xv[NT][kChunk];
@@ -188,10 +189,13 @@ bool run_nt(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_
   auto grid = [&](uint32_t r) { return dim3((rows + kWaves * 2 * r - 1) / (kWaves * 2 * r), (n_tok + NT - 1) / NT); };
   // (the staged row copy at tiles of up to 4 tokens, one row a half-wave: 2048 -> 6144 Q4_K at 8 tokens 22.1 -> 15.5
   // us; at tiles of 8 it lost, 60 -> 70 us at 64 tokens)
-  if (stages<T>() && NT <= 4 && rb % 16 == 0 && rb <= kStgMax && (uintptr_t) w % 16 == 0)
-    kernel<T, NT, 1, true><<<grid(1), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
-  else
-    kernel<T, NT, rows_per<NT>()><<<grid(rows_per<NT>()), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs,
+  if constexpr (stages<T>()) {
+    if (NT <= 4 && rb % 16 == 0 && rb <= kStgMax && (uintptr_t) w % 16 == 0) {
+      kernel<T, NT, 1, true><<<grid(1), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+      return hipGetLastError() == hipSuccess;
+    }
+  }
+  kernel<T, NT, rows_per<NT>()><<<grid(rows_per<NT>()), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs,
                                                                            n_tok, y, ys);
   return hipGetLastError() == hipSuccess;
 }
@@ -200,6 +204,7 @@ template <uint32_t T>
 bool by_tokens(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_t xs, uint32_t n_tok, float* y,
                uint32_t ys, hipStream_t s) {
   if (!w || !x || !y || !rows || !cols || cols % Block<T>::values || cols % kChunk || !n_tok) return false;
+  if (T == kQ5_KR && rows % 16) return false;  // (whole tiles of 16 rows: quant_repack_q5k's)
   if ((n_tok > 1 && (xs < cols || ys < rows)) || xs % kChunk) return false;
   switch (n_tok) {
     case 1: return run_nt<T, 1>(w, rows, cols, x, xs, n_tok, y, ys, s);
@@ -265,7 +270,7 @@ extern "C" OSM_API bool mv_strided(uint32_t type, const void* w, uint32_t rows, 
   switch (type) {
 #define X(t) \
   case t: return mv::by_tokens<t>(w, rows, cols, x, xs, n_tok, y, ys, s);
-    OSM_MV_TYPES(X)
+    OSM_MV_TYPES(X) X(kQ5_KR)  // (Q5_KR the one-matrix product's alone, as the reference's kernels/mv.hip:277)
 #undef X
     default: return false;
   }
