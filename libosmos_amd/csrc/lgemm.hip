@@ -173,6 +173,18 @@ __device__ inline void factors(lbytes b, int j, float& f0, float& f1) {
 // (-(f 1.5 2^23) is exact: f has at most 17 significant bits. for a finite f; a block whose scale d is not finite
 // gives NaN there, where the contract's product is +-inf or NaN)
 constexpr int kBias = 0x4B400000;
+
+// lane n's value of each 16-lane row, to the whole row (DPP row_newbcast; n a compile-time constant once unrolled)
+__device__ inline float row_bcast(float v, int n) {
+  int r = 0;
+  switch (n) {
+#define B(i) \
+  case i: r = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + i, 0xF, 0xF, true); break;
+    B(0) B(1) B(2) B(3) B(4) B(5) B(6) B(7) B(8) B(9) B(10) B(11) B(12) B(13) B(14) B(15)
+#undef B
+  }
+  return __int_as_float(r);
+}
 constexpr float kBiasF = 12582912.0f;
 
 // tokens an MFMA: the A operand's 16 rows are 8 tokens' two halves, row i token i / 2's half i % 2 (a first half's
@@ -181,11 +193,14 @@ constexpr float kBiasF = 12582912.0f;
 // holds D rows 4 (l / 16) .. + 3 of column l % 16 - both halves of tokens 2 (l / 16) and 2 (l / 16) + 1 of its row
 constexpr int kGroup = 8;
 // token groups a pass (G) and waves a workgroup (W) by type and lane count: the waves split the logical lanes, so a
-// wave holds L / W chains x G groups x 2 accumulators, and each decoded block serves G groups. measured on config 5's
-// routing (512 tokens, 250 experts, the busiest 441) at 2048 x 7168 (us): IQ2_XXS G/W 2/4 1609, 1/8 1320, 2/8 1355,
-// 4/8 1582, 2/16 1356; IQ3_XXS 2/4 3159, 2/8 1742, 4/8 1664, 2/16 1413, 1/16 1485; IQ1_M 2/4 2068, 2/8 1426, 2/16
-// 1472; at 7168 x 2048 (16 lanes) IQ2_XXS 2/4 1352, 4/4 1602, 8/4 2598, 2/8 1432. (IQ3_XXS's 16 KB signed codebook
-// and 44 KB slab leave room for two workgroups a CU: it wants the most waves)
+// wave holds L / W chains x G groups x 2 accumulators, and each decoded block serves G groups. one group a pass takes
+// the A-word ring and the shared token-scale loads (the kernel is bound by those loads, not by its decode: a build
+// without the decode ran 1227 us against 1241, one without the A loads 890); two a pass keep one block of lookahead
+// and their occupancy. measured on config 5's routing (512 tokens, 250 experts, the busiest 441), us, 2048 x 7168 /
+// 7168 x 2048, one group (W 8 / 4) against two (W 8 / 4): IQ2_XXS 1156 / 1234 against 1344 / 1360, IQ1_S 1196 / 1337
+// against 1347 / 1509, IQ2_XS 1219 / 1259 against 1368 / 1386, IQ2_S 1587 / 1492 against 1709 / 1501, IQ3_XXS
+// 1514 (7168 x 2048) against 1747, and at 2048 x 7168 two groups of 16 waves 1413 against one of 16 1458 and one of
+// 8 1612; IQ1_M two groups 1433 / 2119, one 2015 / 3169 (its scale decode holds 88 VGPRs: occupancy 5)
 struct Shape {
   int g, w;
 };
@@ -194,10 +209,10 @@ constexpr Shape shape() {
 #ifdef OSM_LG  // (a build-time override, for tuning sweeps)
   return L == 16 ? Shape{OSM_LG16, OSM_LW16} : Shape{OSM_LG32, OSM_LW32};
 #endif
-  if constexpr (L == 16) return {2, 4};
+  if constexpr (T == kIQ1_M) return {2, L == 16 ? 4 : 8};
+  else if constexpr (L == 16) return {1, 4};
   else if constexpr (T == kIQ3_XXS) return {2, 16};
-  else if constexpr (T == kIQ2_XXS) return {1, 8};
-  else return {2, 8};
+  else return {1, 8};
 }
 
 template <uint32_t T>
@@ -222,12 +237,15 @@ struct Lds {
 // wave w takes the blocks s = w (mod W): its chains are the logical lanes ll = w (mod W), L / W accumulators an
 // output; the xor tree's levels L/2 .. W pair chains of one wave (in registers), its levels W/2 .. 1 pair the waves
 // (through LDS) - the same additions as the tree
-template <uint32_t T, int L, int G, int W>
+template <uint32_t T, int L, int G, int W, bool FULL>
 __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __restrict__ w, const int32_t* __restrict__ cnt,
                                                    const int32_t* __restrict__ xrow, uint32_t cols,
                                                    const int8_t* __restrict__ q, const float* __restrict__ d,
                                                    float* __restrict__ y, uint32_t ys) {
   constexpr int kThreads = W * kWave, per = (int) (Block<T>::values / 32), C = L / W, TOK = kGroup * G;
+  // the A ring's depth (a divisor of C: its slots static). measured on config 5's IQ2_XXS gate (us): 1 block ahead
+  // 1239, 2 1146, 4 1195
+  constexpr int PD = C >= 2 ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
   if (!n) return;  // (the whole workgroup)
@@ -265,64 +283,152 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
   for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
     __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
     const int groups = (int) ((n - c0 + kGroup - 1) / kGroup) < G ? (int) ((n - c0 + kGroup - 1) / kGroup) : G;
-    uint32_t voff[G], xoff[G][2];
+    uint32_t voff[G], xoff[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
       const uint32_t t = c0 + g * kGroup + col / 2;
       voff[g] = lives && t < n ? t * cols + 8 * quad : 0x80000000u;
-#pragma unroll
-      for (int p = 0; p < 2; p++) {
-        const uint32_t to = c0 + g * kGroup + ot + p;
-        xoff[g][p] = to < n ? to * nblk * 4 : 0x80000000u;
-      }
+      const uint32_t to = c0 + g * kGroup + ot + (col & 1);
+      xoff[g] = to < n ? to * nblk * 4 : 0x80000000u;
     }
     float acc[C][G][2];
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
       for (int g = 0; g < G; g++) acc[c][g][0] = acc[c][g][1] = 0.0f;
-    // the A words and token scales of the wave's next block, loaded one block ahead
-    long an[G];
-    float xn[G][2];
-    auto aload = [&](uint32_t s) __attribute__((always_inline)) {
+    if constexpr (G == 1) {
+      // the A words of the wave's blocks, PD blocks ahead (a ring of PD register sets: the loads' latency is the
+      // kernel's bound, not its arithmetic). every load is made, on every path (a zero of the layout, or a group past
+      // the count, at an offset past the descriptor's end: zeros, no access), so the loads in flight are counted
+      // exactly and each wait is for the oldest alone
+      long an[PD][G];
+      auto aload = [&](int slot, uint32_t s) __attribute__((always_inline)) {
+  #pragma unroll
+        for (int g = 0; g < G; g++)
+          an[slot][g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
+      };
+      // the token scales of a round's C blocks (s0 + W c), one load a lane a round: lane col of a 16-lane row holds
+      // token ot + (col & 1)'s scale of block s0 + W (col / 2) (col / 2 < C), and each block's two broadcast from it
+      const uint32_t kc = (uint32_t) (col / 2) < (uint32_t) C ? (uint32_t) (col / 2) : (uint32_t) (C - 1);
+      // (the first round's scales first, then the ring: in the order every round issues them, scales before A words)
+      float sn[G];
+      {
+        const uint32_t sb = wave + W * kc < nblk ? wave + W * kc : nblk - 1;  // (per lane: a vector offset)
+  #pragma unroll
+        for (int g = 0; g < G; g++)
+          sn[g] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff[g] == 0x80000000u ? xoff[g] : xoff[g] + sb * 4, 0, 0));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // (kept in that order, the ring in slot order)
+  #pragma unroll
+      for (int i = 0; i < PD; i++) {
+        aload(i, wave + W * i < nblk ? wave + W * i : nblk - 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // (no value is copied from round to round: each ring slot is reloaded only after the MFMA that reads it, and the
+      // rounds take their scales from two register sets in turn, each round loading the next round's into the other -
+      // a loop-carried copy would wait for its load, and with it every load made since)
+      float sa[G], sb2[G];
+  #pragma unroll
+      for (int g = 0; g < G; g++) sa[g] = sn[g];
+      auto round = [&](uint32_t s0, float (&sc)[G], float (&nx_sc)[G]) __attribute__((always_inline)) {
+        {
+          const uint32_t nx = s0 + L < nblk ? s0 + L : s0;  // (the next round's, a round ahead)
+          const uint32_t sb = nx + W * kc < nblk ? nx + W * kc : nblk - 1;
+  #pragma unroll
+          for (int g = 0; g < G; g++)
+            nx_sc[g] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff[g] == 0x80000000u ? xoff[g] : xoff[g] + sb * 4, 0, 0));
+        }
+  #pragma unroll
+        for (int c = 0; c < C; c++) {
+          const uint32_t s = s0 + W * c;  // logical lane wave + W c
+          if (!FULL && s >= nblk) break;  // (uniform; FULL: every round whole)
+          const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+          const int j = (int) (s % per);
+          uint32_t w0, w1;
+          chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+          const long b = (long) (((uint64_t) w1 << 32) | w0);
+          float f0, f1;
+          factors<T>((lbytes) blk, j, f0, f1);
+          const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+          v4i D[G];
+  #pragma unroll
+          for (int g = 0; g < G; g++)
+            if (g < groups) D[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD][g], b, bias, 0, 0, 0);
+          aload(c % PD, s + W * PD < nblk ? s + W * PD : s);  // (past the last block: loaded again, unused - no branch)
+  #pragma unroll
+          for (int g = 0; g < G; g++) {
+            if (g < groups) {
+              const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[g][0]), n0),
+                                          __builtin_fmaf(f1, __int_as_float(D[g][1]), n1));
+              const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[g][2]), n0),
+                                          __builtin_fmaf(f1, __int_as_float(D[g][3]), n1));
+              acc[c][g][0] = __builtin_fmaf(row_bcast(sc[g], 2 * c), s0_, acc[c][g][0]);
+              acc[c][g][1] = __builtin_fmaf(row_bcast(sc[g], 2 * c + 1), s1_, acc[c][g][1]);
+            }
+          }
+        }
+      };
+      for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += 2 * L) {
+        round(s0, sa, sb2);
+        if (s0 + L >= nblk) break;
+        round(s0 + L, sb2, sa);
+      }
+    } else {
+      // two or more groups a pass (the types whose decode is dearest: each decoded block serves both): the A words and
+      // token scales one block ahead, each lane loading its two outputs' scales (a ring here costs these kernels
+      // their occupancy)
+      uint32_t xo[G][2];
 #pragma unroll
       for (int g = 0; g < G; g++)
-        if (g < groups) {
-          an[g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
 #pragma unroll
-          for (int p = 0; p < 2; p++)
-            xn[g][p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff[g][p], s * 4, 0));
+        for (int p = 0; p < 2; p++) {
+          const uint32_t to = c0 + g * kGroup + ot + p;
+          xo[g][p] = to < n ? to * nblk * 4 : 0x80000000u;
         }
-    };
-    aload((uint32_t) wave);
-    for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += L) {
+      long an[G];
+      float xn[G][2];
+      auto aload = [&](uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
-      for (int c = 0; c < C; c++) {
-        const uint32_t s = s0 + W * c;  // logical lane wave + W c
-        if (s >= nblk) break;           // (uniform)
-        long a[G];
-        float x[G][2];
-#pragma unroll
-        for (int g = 0; g < G; g++) a[g] = an[g], x[g][0] = xn[g][0], x[g][1] = xn[g][1];
-        aload(s + W < nblk ? s + W : s);  // (the last block: loaded again, unused - no branch)
-        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
-        const int j = (int) (s % per);
-        uint32_t w0, w1;
-        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
-        const long b = (long) (((uint64_t) w1 << 32) | w0);
-        float f0, f1;
-        factors<T>((lbytes) blk, j, f0, f1);
-        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
-#pragma unroll
-        for (int g = 0; g < G; g++) {
+        for (int g = 0; g < G; g++)
           if (g < groups) {
-            const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[g], b, bias, 0, 0, 0);
-            const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0),
-                                        __builtin_fmaf(f1, __int_as_float(D[1]), n1));
-            const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0),
-                                        __builtin_fmaf(f1, __int_as_float(D[3]), n1));
-            acc[c][g][0] = __builtin_fmaf(x[g][0], s0_, acc[c][g][0]);
-            acc[c][g][1] = __builtin_fmaf(x[g][1], s1_, acc[c][g][1]);
+            an[g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+              xn[g][p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(dr, xo[g][p], s * 4, 0));
+          }
+      };
+      aload((uint32_t) wave);
+      for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += L) {
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          const uint32_t s = s0 + W * c;  // logical lane wave + W c
+          if (!FULL && s >= nblk) break;  // (uniform)
+          long a[G];
+          float x[G][2];
+#pragma unroll
+          for (int g = 0; g < G; g++) a[g] = an[g], x[g][0] = xn[g][0], x[g][1] = xn[g][1];
+          aload(s + W < nblk ? s + W : s);  // (the last block: loaded again, unused - no branch)
+          const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+          const int j = (int) (s % per);
+          uint32_t w0, w1;
+          chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+          const long b = (long) (((uint64_t) w1 << 32) | w0);
+          float f0, f1;
+          factors<T>((lbytes) blk, j, f0, f1);
+          const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+#pragma unroll
+          for (int g = 0; g < G; g++) {
+            if (g < groups) {
+              const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[g], b, bias, 0, 0, 0);
+              const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0),
+                                          __builtin_fmaf(f1, __int_as_float(D[1]), n1));
+              const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0),
+                                          __builtin_fmaf(f1, __int_as_float(D[3]), n1));
+              acc[c][g][0] = __builtin_fmaf(x[g][0], s0_, acc[c][g][0]);
+              acc[c][g][1] = __builtin_fmaf(x[g][1], s1_, acc[c][g][1]);
+            }
           }
         }
       }
@@ -368,7 +474,7 @@ bool launch(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint3
             uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
   const Lds<G, W> l((uint32_t) row_bytes<T>(cols), grid_bytes_of<T>());
   if (l.total > 160 * 1024) return false;
-  auto k = kernel<T, L, G, W>;
+  auto k = (cols / 32) % L == 0 ? kernel<T, L, G, W, true> : kernel<T, L, G, W, false>;
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
