@@ -91,6 +91,22 @@ constexpr Grids make_grids() {
 // ---- loads: GGUF blocks are 2-byte aligned (their sizes are even), so wider words come from aligned dwords ----
 __device__ inline uint32_t ld8(const uint8_t* p) { return *p; }
 __device__ inline uint32_t ld16(const uint8_t* p) { return *(const uint16_t*) p; }
+// a load through the global address space: a pointer the compiler cannot place (one read from a table, a struct's)
+// would otherwise be a flat load, which also counts against the LDS wait counter - every wait for an LDS read would
+// then wait for it too
+// entry i of a device table of pointers to global memory (weight matrices' tables), read as a global-space pointer:
+// every load derived from it is then a global load, where a pointer read as a generic one makes flat loads (which
+// also count against the LDS wait counter, so each wait for an LDS read would wait for them too)
+template <typename T>
+__device__ inline T* table_at(T* const* tab, uint32_t i) {
+  typedef __attribute__((address_space(1))) T* G;
+  const G g = ((const G*) tab)[i];
+  return (T*) g;
+}
+template <typename V>
+__device__ inline V gload(const void* p) {
+  return *(const __attribute__((address_space(1))) V*) p;
+}
 __device__ inline uint32_t ld32(const uint8_t* p) { return ld16(p) | ld16(p + 2) << 16; }
 __device__ inline float f16(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short) bits)); }
 

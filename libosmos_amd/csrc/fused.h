@@ -650,8 +650,8 @@ __device__ __forceinline__ void gu1_item(const GuArgs& a, const G1Tab& tb, uint3
   __builtin_amdgcn_sched_barrier(0);
   u32x4 wv[2 * S];
   if constexpr (TAB) {
-    const uint8_t* gb = tb.wg[m] + (uint64_t) r0 * rb;
-    const uint8_t* ub = tb.wu[m] + (uint64_t) r0 * rb;
+    const uint8_t* gb = table_at(tb.wg, m) + (uint64_t) r0 * rb;
+    const uint8_t* ub = table_at(tb.wu, m) + (uint64_t) r0 * rb;
     if ((((uintptr_t) gb | (uintptr_t) ub) & 15) == 0) {
 #pragma unroll
       for (uint32_t u = 0; u < (uint32_t) S; u++) wv[u] = wload((const u32x4*) gb + idx[u]), wv[S + u] = wload((const u32x4*) ub + idx[u]);

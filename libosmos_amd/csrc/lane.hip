@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   const uint32_t n = n_all - z0 < (uint32_t) NT ? n_all - z0 : NT;
   const uint32_t r0 = (uint32_t) xrow[m] + z0;
   const uint64_t rbytes = row_bytes<T>(cols);
-  const uint8_t* rb = w[m] + (uint64_t) (row < rows ? row : 0) * rbytes;
+  const uint8_t* rb = table_at(w, m) + (uint64_t) (row < rows ? row : 0) * rbytes;
   // STG (the matrix 16-aligned, a row a whole number of 16-byte words within a slot: known here, uniform a matrix):
   // the row group first copies its row into its own LDS slot with 16-byte loads, then decodes from there
   if constexpr (STG) {
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(NTH) void wide_kernel(const uint8_t* const* __restr
   if (!cnt[m]) return;  // (an entry past a device-built table's live ones: nothing read or written)
   const int t = threadIdx.x, rl = t / R, p = t % R;
   const uint32_t row = blockIdx.x * RW + rl;
-  const uint8_t* src = w[m] + (uint64_t) (row < rows ? row : 0) * rb + CB * p;
+  const uint8_t* src = table_at(w, m) + (uint64_t) (row < rows ? row : 0) * rb + CB * p;
   uint32_t W[36];
   if constexpr (CB % 16) {
     const uintptr_t a0 = (uintptr_t) w[m] & ~(uintptr_t) 15, at = (uintptr_t) src;
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kThreads) void one_kernel(const uint8_t* const* __r
                                                        float* __restrict__ y, uint32_t ys) {
   const uint32_t m = blockIdx.y, row = blockIdx.x * OneShape<L>::rows + threadIdx.x / OneShape<L>::group;
   if (!cnt[m] || row >= rows) return;  // (no token; or a group past the rows: its tree's partners are its own)
-  const uint8_t* wm = w[m];
+  const uint8_t* wm = table_at(w, m);
   // (the staged form needs the matrix 16-aligned: known only here, a uniform choice a matrix)
   if (STG && (uintptr_t) wm % 16 == 0)
     one_row<T, L, STG>(wm, row, (uint32_t) xrow[m], xin, cols, q, d, y, ys);
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(const uint8_t* const*
   const uint32_t n = n_all - z0 < (uint32_t) NT ? n_all - z0 : NT;
   const uint32_t nblk = cols / 32, r0 = (uint32_t) xrow[m] + z0;
   const uint64_t off = (uint64_t) (row < rows ? row : 0) * row_bytes<T>(cols);
-  const uint8_t *rg = wg[m] + off, *ru = wu[m] + off;
+  const uint8_t *rg = table_at(wg, m) + off, *ru = table_at(wu, m) + off;
   uint64_t xr[NT];
   in_rows<NT>(xin, r0, n, xr);
   float ag[NT], au[NT];

@@ -256,7 +256,7 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
   const uint32_t rb = (uint32_t) row_bytes<T>(cols);
   const Lds<G, W> L_(rb, grid_bytes_of<T>());
   {  // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
-    const u32x4* src = (const u32x4*) (w[m] + (uint64_t) row0 * rb);
+    const u32x4* src = (const u32x4*) (table_at(w, m) + (uint64_t) row0 * rb);
     const uint32_t nw = 16 * rb / 16;
     for (uint32_t i = threadIdx.x; i < nw; i += kThreads) ((u32x4*) (smem + L_.slab))[i] = src[i];
     constexpr uint32_t ng = grid_bytes_of<T>() / 16;

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
   float* y = a.y;
   uint32_t n = a.n;
   if (a.wt) {
-    w = a.wt[m], n = (uint32_t) a.cnt[m];
+    w = table_at(a.wt, m), n = (uint32_t) a.cnt[m];
     x16 += a.xoff[m], y += a.yoff[m];
   }
   const uint32_t t0 = blockIdx.z * kTile * CT, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, q = lane / 16;
@@ -240,14 +240,14 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
     if constexpr (kTiled) {  // (every round whole: cols a multiple of the block)
       const uint8_t* base = w + (uint64_t) r * kTile * kRb;
 #pragma unroll
-      for (uint32_t u = 0; u < kPer; u++) wr[u] = *(const word*) (base + woff[u]);
+      for (uint32_t u = 0; u < kPer; u++) wr[u] = gload<word>(base + woff[u]);
     } else {
       const uint32_t lim = (a.cols - r * kRv) / Block<T>::values * Block<T>::bytes;  // the round's bytes a row
       const uint8_t* base = w + (uint64_t) r * kRb;
 #pragma unroll
       for (uint32_t u = 0; u < kPer; u++) {
         const uint32_t o = (u * kThreads + threadIdx.x) % kWr * WB;
-        wr[u] = *(const word*) (base + woff[u] - (o < lim ? 0 : o - (lim - WB)));  // (past a short round: its last word)
+        wr[u] = gload<word>(base + woff[u] - (o < lim ? 0 : o - (lim - WB)));  // (past a short round: its last word)
       }
     }
   };
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
   fill_tab<T>(tab);
   load(0);
   store(0);
-  if (nr > 1) load(1);
+  load(nr > 1 ? 1 : 0);  // (every load made: the in-flight count exact on every path)
   __syncthreads();
   const _Float16* xb = x16 + x16_at(t0 + lane % 16, 8 * q, a.xts);
   f32x4 acc[RT][CT];
@@ -267,10 +267,20 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
   for (int rt = 0; rt < RT; rt++)
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) acc[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // the activations of the wave's next step (its 32 columns of each token tile), loaded a step ahead: every load made
+  // (a tile past the live ones reads tile 0 again, a step past the matrix this step's columns), so the loads in flight
+  // are counted exactly and each wait is for that one
+  half8 bn[CT];
+  auto xload = [&](uint32_t kk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+      bn[ct] = gload<half8>(xb + (uint64_t) (ct < tiles ? ct : 0) * kTile * a.xts + (kk / 16) * 256);
+  };
+  xload(wave * SL < a.cols ? wave * SL : 0);
   for (uint32_t r = 0; r < nr; r++) {
     const int buf = (int) (r % 2);
     if (r + 1 < nr) store(buf ^ 1);  // (buffer buf ^ 1's last reads were before the previous barrier)
-    if (r + 2 < nr) load(r + 2);
+    load(r + 2 < nr ? r + 2 : nr - 1);  // (past the last round: the last again, not stored)
     const uint32_t k_slab = r * kRv + wave * SL;  // this wave's slab of the round
     if (k_slab < a.cols) {  // (uniform in the wave)
 #pragma unroll
@@ -294,10 +304,17 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
           }
         }
         const uint32_t kk = k_slab + k0;
+        half8 bc[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) bc[ct] = bn[ct];
+        {
+          const uint32_t nx = k0 + kStep < SL ? kk + kStep : k_slab + kRv;  // the wave's next step
+          xload(nx < a.cols ? nx : kk);
+        }
 #pragma unroll
         for (int ct = 0; ct < CT; ct++)
           if (ct < tiles) {  // (uniform) the tiles that exist
-            const half8 bv = *(const half8*) (xb + (uint64_t) ct * kTile * a.xts + (kk / 16) * 256);
+            const half8 bv = bc[ct];
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
               acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt], bv, acc[rt][ct], 0, 0, 0);

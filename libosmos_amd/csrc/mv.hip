@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void group_kernel(const uint8_t* const* _
                                                          uint32_t cols, const float* __restrict__ x, uint32_t x_mat,
                                                          uint32_t x_div, float* __restrict__ y) {
   const uint32_t m = blockIdx.y;
-  const uint8_t* wm = w[m];
+  const uint8_t* wm = table_at(w, m);
   const float* xm = x + (uint64_t) (m / x_div) * x_mat;
   if constexpr (stages<T>() && R == 1) {  // (the matrix's alignment is known only here: a uniform choice per matrix)
     const uint32_t rb = (uint32_t) row_bytes<T>(cols);
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void group_tok_kernel(const uint8_t* cons
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
   if (!n) return;
   const uint64_t r0 = (uint64_t) xrow[m];
-  rows_of<T, NT, R>(w[m], rows, cols, x + r0 * xs, xs, y + r0 * ys, ys, n < (uint32_t) NT ? n : NT);
+  rows_of<T, NT, R>(table_at(w, m), rows, cols, x + r0 * xs, xs, y + r0 * ys, ys, n < (uint32_t) NT ? n : NT);
 }
 
 // rows a half-wave: the tiling alone, never the bits (one token: a row a half-wave, for as many waves as the rows give)
