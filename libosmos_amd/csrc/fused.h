@@ -921,10 +921,15 @@ __global__ __launch_bounds__(kWave * W) void gub_kernel(GuArgs a) {
   int32_t* toks = (int32_t*) (smem + LD::toks);  // [0, kMaxTok): the expert's picks in token order; [kMaxTok]: count
   if (threadIdx.x < kWave) {  // wave 0, a lane a token: its pick of e if any, placed by the earlier tokens' count
     int32_t pk = -1;
-    if (threadIdx.x < a.n_tok)
-      for (uint32_t j = 0; j < a.k; j++)
-        if ((n <= 2 * kThreads ? sid[threadIdx.x * a.k + j] : ids[threadIdx.x * a.k + j]) == e)
-          pk = (int32_t) (threadIdx.x * a.k + j);
+    if (threadIdx.x < a.n_tok) {  // (a uniform choice of table: LDS reads or global ones, never a flat load of either)
+      if (n <= 2 * kThreads) {
+        for (uint32_t j = 0; j < a.k; j++)
+          if (sid[threadIdx.x * a.k + j] == e) pk = (int32_t) (threadIdx.x * a.k + j);
+      } else {
+        for (uint32_t j = 0; j < a.k; j++)
+          if (ids[threadIdx.x * a.k + j] == e) pk = (int32_t) (threadIdx.x * a.k + j);
+      }
+    }
     const uint64_t has = __ballot(pk >= 0);
     if (pk >= 0) toks[__builtin_popcountll(has & ((1ull << threadIdx.x) - 1))] = pk;
     if (threadIdx.x == 0) toks[kMaxTok] = __builtin_popcountll(has);
