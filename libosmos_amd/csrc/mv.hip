@@ -35,9 +35,19 @@ template <uint32_t T> constexpr bool stages() {
   return T == kQ2_K || T == kQ4_K || T == kQ5_K || T == kIQ2_XXS || T == kIQ2_XS || T == kIQ2_S || T == kIQ3_XXS ||
          T == kIQ1_S || T == kIQ1_M || T == kIQ4_XS || T == kIQ4_NL;
 }
-template <uint32_t T, int NT, int R, bool STG = false>
+// XL (one token): x already copied into the workgroup's LDS (xl): the 8 rows of a workgroup read it there, not each
+// from L2 - the same values, so the same bits
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(3))) f32x4v lds_f4;
+constexpr uint32_t kXlMax = 4096;  // x floats a workgroup copies at most
+// the types that take it: measured at one token on 8192 x 2048 (us, x from L2 / from LDS): Q4_0 6.43 / 5.69, BF16
+// 8.44 / 8.16; slower for the rest (F32 14.1 / 14.1, Q8_0 8.11 / 8.25, Q3_K 8.18 / 10.85, Q4_K 7.22 / 9.16, Q6_K
+// 9.81 / 13.32, IQ2_XXS 7.23 / 7.46, IQ4_NL 7.72 / 9.94 ...: the compiler keeps fewer of their weight loads in flight)
+template <uint32_t T> constexpr bool x_in_lds() { return T == kQ4_0 || T == kBF16; }
+template <uint32_t T, int NT, int R, bool STG = false, bool XL = false>
 __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* __restrict__ x,
-                               uint32_t xs, float* __restrict__ y, uint32_t ys, uint32_t live) {
+                               uint32_t xs, float* __restrict__ y, uint32_t ys, uint32_t live,
+                               lds_f4* xl = nullptr) {
   const int lane = threadIdx.x % kHalf;
   const uint32_t row0 = ((blockIdx.x * kWaves + threadIdx.x / kWave) * 2 + (threadIdx.x % kWave) / kHalf) * R;
   // SW (an even token tile): the two half-waves hold the same chunks of different rows, so each loads half of the
@@ -107,8 +117,15 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
     } else {
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const float4 a = ((const float4*) (xt[t] + (uint64_t) c * kChunk))[0];
-        const float4 b = ((const float4*) (xt[t] + (uint64_t) c * kChunk))[1];
+        float4 a, b;
+        if constexpr (XL) {
+          static_assert(NT == 1, "x in LDS: one token");
+          const f32x4v va = xl[2 * c], vb = xl[2 * c + 1];
+          a = make_float4(va.x, va.y, va.z, va.w), b = make_float4(vb.x, vb.y, vb.z, vb.w);
+        } else {
+          a = ((const float4*) (xt[t] + (uint64_t) c * kChunk))[0];
+          b = ((const float4*) (xt[t] + (uint64_t) c * kChunk))[1];
+        }
         xv[t][0] = a.x, xv[t][1] = a.y, xv[t][2] = a.z, xv[t][3] = a.w;
         xv[t][4] = b.x, xv[t][5] = b.y, xv[t][6] = b.z, xv[t][7] = b.w;
       }
@@ -145,6 +162,24 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* __restrict__ w
                                                    const float* __restrict__ x, uint32_t xs, uint32_t n_tok,
                                                    float* __restrict__ y, uint32_t ys) {
   const uint32_t t0 = blockIdx.y * NT, live = n_tok - t0 < (uint32_t) NT ? n_tok - t0 : NT;
+  if constexpr (NT == 1 && x_in_lds<T>()) {
+    if (cols <= kXlMax) {  // (uniform) the token's row into LDS: every load first, then the stores
+      __shared__ __attribute__((aligned(16))) float xsm[kXlMax];
+      constexpr int U = (int) (kXlMax / 4 / kThreads);
+      const float4* src = (const float4*) (x + (uint64_t) t0 * xs);
+      const uint32_t nw = cols / 4;
+      float4 r[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) r[u] = src[min(threadIdx.x + u * kThreads, nw - 1)];
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        if (threadIdx.x + u * kThreads < nw) ((float4*) xsm)[threadIdx.x + u * kThreads] = r[u];
+      __syncthreads();
+      rows_of<T, NT, R, STG, true>(w, rows, cols, x + (uint64_t) t0 * xs, xs, y + (uint64_t) t0 * ys, ys, live,
+                                   (lds_f4*) xsm);
+      return;
+    }
+  }
   rows_of<T, NT, R, STG>(w, rows, cols, x + (uint64_t) t0 * xs, xs, y + (uint64_t) t0 * ys, ys, live);
 }
 
