@@ -157,10 +157,10 @@ __device__ inline void rows_of(const uint8_t* __restrict__ w, uint32_t rows, uin
 }
 
 // one matrix, n_tok tokens in tiles of NT over blockIdx.y
-template <uint32_t T, int NT, int R, bool STG = false>
-__global__ __launch_bounds__(kThreads) void kernel(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols,
-                                                   const float* __restrict__ x, uint32_t xs, uint32_t n_tok,
-                                                   float* __restrict__ y, uint32_t ys) {
+template <uint32_t T, int NT, int R, bool STG>
+__device__ __forceinline__ void tokens_item(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols,
+                                            const float* __restrict__ x, uint32_t xs, uint32_t n_tok,
+                                            float* __restrict__ y, uint32_t ys) {
   const uint32_t t0 = blockIdx.y * NT, live = n_tok - t0 < (uint32_t) NT ? n_tok - t0 : NT;
   if constexpr (NT == 1 && x_in_lds<T>()) {
     if (cols <= kXlMax) {  // (uniform) the token's row into LDS: every load first, then the stores
@@ -181,6 +181,25 @@ __global__ __launch_bounds__(kThreads) void kernel(const uint8_t* __restrict__ w
     }
   }
   rows_of<T, NT, R, STG>(w, rows, cols, x + (uint64_t) t0 * xs, xs, y + (uint64_t) t0 * ys, ys, live);
+}
+
+template <uint32_t T, int NT, int R, bool STG = false>
+__global__ __launch_bounds__(kThreads) void kernel(const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols,
+                                                   const float* __restrict__ x, uint32_t xs, uint32_t n_tok,
+                                                   float* __restrict__ y, uint32_t ys) {
+  tokens_item<T, NT, R, STG>(w, rows, cols, x, xs, n_tok, y, ys);
+}
+// the same with the compiler's register budget set for 4 waves a SIMD (a one-token launch has about that many): it
+// then keeps more of a lane's chunk loads in flight. measured at one token (us, 8192 x 2048 / 6144 x 2048): Q4_0
+// 5.68 / 5.29 -> 5.10 / 4.68, F32 14.1 / 11.3 -> 13.0 / 10.5, Q8_0 6.94 -> 6.42 (6144), Q3_K 6.99 -> 6.70, the IQ2 / IQ1 /
+// K types 1-3 % faster; IQ4_NL 7.64 -> 9.47, Q6_K 9.78 -> 9.96 and IQ2_XS 5.79 -> 5.93 (6144) slower, so they keep
+// the first
+template <uint32_t T> constexpr bool budget4() { return T != kIQ4_NL && T != kQ6_K && T != kIQ2_XS; }
+template <uint32_t T, int NT, int R, bool STG = false>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void kernel4(
+    const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* __restrict__ x, uint32_t xs,
+    uint32_t n_tok, float* __restrict__ y, uint32_t ys) {
+  tokens_item<T, NT, R, STG>(w, rows, cols, x, xs, n_tok, y, ys);
 }
 
 // n matrices of one shape (blockIdx.y the matrix): x at x + (m / x_div) x_mat, y at y + m rows
@@ -224,14 +243,22 @@ bool run_nt(const void* w, uint32_t rows, uint32_t cols, const float* x, uint32_
   auto grid = [&](uint32_t r) { return dim3((rows + kWaves * 2 * r - 1) / (kWaves * 2 * r), (n_tok + NT - 1) / NT); };
   // (the staged row copy at tiles of up to 4 tokens, one row a half-wave: 2048 -> 6144 Q4_K at 8 tokens 22.1 -> 15.5
   // us; at tiles of 8 it lost, 60 -> 70 us at 64 tokens)
+  constexpr bool B4 = NT == 1 && budget4<T>();
   if constexpr (stages<T>()) {
     if (NT <= 4 && rb % 16 == 0 && rb <= kStgMax && (uintptr_t) w % 16 == 0) {
-      kernel<T, NT, 1, true><<<grid(1), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+      if constexpr (B4)
+        kernel4<T, NT, 1, true><<<grid(1), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
+      else
+        kernel<T, NT, 1, true><<<grid(1), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs, n_tok, y, ys);
       return hipGetLastError() == hipSuccess;
     }
   }
-  kernel<T, NT, rows_per<NT>()><<<grid(rows_per<NT>()), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs,
-                                                                           n_tok, y, ys);
+  if constexpr (B4)
+    kernel4<T, NT, rows_per<NT>()><<<grid(rows_per<NT>()), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs,
+                                                                              n_tok, y, ys);
+  else
+    kernel<T, NT, rows_per<NT>()><<<grid(rows_per<NT>()), kThreads, 0, s>>>((const uint8_t*) w, rows, cols, x, xs,
+                                                                             n_tok, y, ys);
   return hipGetLastError() == hipSuccess;
 }
 
