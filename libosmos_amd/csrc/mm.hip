@@ -196,7 +196,10 @@ template <uint32_t T> KSplit shape_of(uint32_t cols, bool group) {
 // slots with the same columns, so each step is its 32 values' dot product whatever order the unit takes them in.
 // then the partitions' tiles are summed in order through LDS. RT and CT are the tiling alone: the same sums
 template <uint32_t T, uint32_t SL, int W, int CT, int RT, int WB>
-__global__ __launch_bounds__(W * kWave) void kernel(Args a) {
+// (IQ2_XXS on 4-byte staging words held to 128 VGPRs, 4 waves a SIMD: config 5's gate 761-783 -> 733 us, no spills;
+// the other instances spill at that budget)
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(T == kIQ2_XXS && WB == 4 ? 4 : 1)))
+void kernel(Args a) {
   typedef typename std::conditional<WB == 4, uint32_t, uint16_t>::type word;
   constexpr int kThreads = W * kWave;
   constexpr uint32_t kRows = kTile * RT;                                // the workgroup's rows
@@ -270,13 +273,15 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
   // the activations of the wave's next step (its 32 columns of each token tile), loaded a step ahead: every load made
   // (a tile past the live ones reads tile 0 again, a step past the matrix this step's columns), so the loads in flight
   // are counted exactly and each wait is for that one
+  // (not for the shapes whose registers it would spill: Q8_0's and Q4_K's four row tiles by two token tiles)
+  constexpr bool kXPre = !(RT == 4 && CT == 2 && (T == kQ8_0 || T == kQ4_K));
   half8 bn[CT];
   auto xload = [&](uint32_t kk) __attribute__((always_inline)) {
 #pragma unroll
     for (int ct = 0; ct < CT; ct++)
       bn[ct] = gload<half8>(xb + (uint64_t) (ct < tiles ? ct : 0) * kTile * a.xts + (kk / 16) * 256);
   };
-  xload(wave * SL < a.cols ? wave * SL : 0);
+  if constexpr (kXPre) xload(wave * SL < a.cols ? wave * SL : 0);
   for (uint32_t r = 0; r < nr; r++) {
     const int buf = (int) (r % 2);
     if (r + 1 < nr) store(buf ^ 1);  // (buffer buf ^ 1's last reads were before the previous barrier)
@@ -305,16 +310,18 @@ __global__ __launch_bounds__(W * kWave) void kernel(Args a) {
         }
         const uint32_t kk = k_slab + k0;
         half8 bc[CT];
+        if constexpr (kXPre) {
 #pragma unroll
-        for (int ct = 0; ct < CT; ct++) bc[ct] = bn[ct];
-        {
+          for (int ct = 0; ct < CT; ct++) bc[ct] = bn[ct];
           const uint32_t nx = k0 + kStep < SL ? kk + kStep : k_slab + kRv;  // the wave's next step
           xload(nx < a.cols ? nx : kk);
         }
 #pragma unroll
         for (int ct = 0; ct < CT; ct++)
           if (ct < tiles) {  // (uniform) the tiles that exist
-            const half8 bv = bc[ct];
+            half8 bv;
+            if constexpr (kXPre) bv = bc[ct];
+            else bv = gload<half8>(xb + (uint64_t) ct * kTile * a.xts + (kk / 16) * 256);
 #pragma unroll
             for (int rt = 0; rt < RT; rt++)
               acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[rt], bv, acc[rt][ct], 0, 0, 0);
