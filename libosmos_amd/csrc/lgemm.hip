@@ -15,7 +15,8 @@
 // accumulator) so each product is one fma. the float steps then run per output in the contract's order. the W waves
 // split the logical lanes (wave w the chains ll = w mod W, blocks s = w mod W), so a wave keeps L / W chains an output
 // in registers; the xor tree is finished across the waves through LDS with the same additions (fadd commutes exactly).
-// groups of 8 tokens waste at most 7 token slots a matrix (prefill's many small experts).
+// groups of 8 tokens waste at most 7 token slots a matrix (prefill's many small experts). kernel16 (most types) takes
+// 16 tokens a pass instead, one token a lane in the A operand and the halves split on the weights' side (below).
 #include "lanedec.h"
 
 extern "C" {
@@ -192,15 +193,16 @@ constexpr float kBiasF = 12582912.0f;
 // operand the block's full 32 codes of 16 weight rows: one MFMA gives both half-dots of 8 tokens x 16 rows, and lane l
 // holds D rows 4 (l / 16) .. + 3 of column l % 16 - both halves of tokens 2 (l / 16) and 2 (l / 16) + 1 of its row
 constexpr int kGroup = 8;
-// token groups a pass (G) and waves a workgroup (W) by type and lane count: the waves split the logical lanes, so a
-// wave holds L / W chains x G groups x 2 accumulators, and each decoded block serves G groups. one group a pass takes
-// the A-word ring and the shared token-scale loads (the kernel is bound by those loads, not by its decode: a build
-// without the decode ran 1227 us against 1241, one without the A loads 890); two a pass keep one block of lookahead
-// and their occupancy. measured on config 5's routing (512 tokens, 250 experts, the busiest 441), us, 2048 x 7168 /
-// 7168 x 2048, one group (W 8 / 4) against two (W 8 / 4): IQ2_XXS 1156 / 1234 against 1344 / 1360, IQ1_S 1196 / 1337
-// against 1347 / 1509, IQ2_XS 1219 / 1259 against 1368 / 1386, IQ2_S 1587 / 1492 against 1709 / 1501, IQ3_XXS
-// 1514 (7168 x 2048) against 1747, and at 2048 x 7168 two groups of 16 waves 1413 against one of 16 1458 and one of
-// 8 1612; IQ1_M two groups 1433 / 2119, one 2015 / 3169 (its scale decode holds 88 VGPRs: occupancy 5)
+// token groups a pass (G) and waves a workgroup (W) by type and lane count. G = 1: kernel16, 16 tokens a pass (the
+// halves split on the weights' side); G = 2: kernel, two groups of 8 a pass (each decoded block serving both). the
+// kernels are bound by their loads, not their decode (a build of kernel without the decode ran 1227 us against 1241,
+// one without its A loads 890): kernel16 halves the A loads a full group issues. measured on config 5's routing (512
+// tokens, 250 experts, the busiest 441), us, 2048 x 7168 / 7168 x 2048: kernel16 (W 8 / 4) IQ2_XXS 1098 / 1201,
+// IQ1_S 1133 / 1283, IQ2_XS 1136 / 1260, IQ2_S 1399 / 1434, IQ3_XXS 1260 (W 16; 1326 at 8) / 1421; kernel with one group
+// of 8 a pass 1161 / 1223, 1188 / 1325, 1214 / 1254, 1583 / 1497, 1612 / 1508 (it was 1308 / 1362 for IQ2_XXS before
+// its loads were reworked); with two groups 1344 / 1360, 1347 / 1509, 1368 / 1386, 1709 / 1501, 1411 (W 16) / 1747;
+// IQ1_M two groups 1426 / 2107 against kernel16's 1450 / 2113 and one group's 2015 / 3169 (its scale decode holds 88
+// VGPRs: occupancy 5)
 struct Shape {
   int g, w;
 };
@@ -211,7 +213,7 @@ constexpr Shape shape() {
 #endif
   if constexpr (T == kIQ1_M) return {2, L == 16 ? 4 : 8};
   else if constexpr (L == 16) return {1, 4};
-  else if constexpr (T == kIQ3_XXS) return {2, 16};
+  else if constexpr (T == kIQ3_XXS) return {1, 16};
   else return {1, 8};
 }
 
@@ -243,9 +245,7 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
                                                    const int8_t* __restrict__ q, const float* __restrict__ d,
                                                    float* __restrict__ y, uint32_t ys) {
   constexpr int kThreads = W * kWave, per = (int) (Block<T>::values / 32), C = L / W, TOK = kGroup * G;
-  // the A ring's depth (a divisor of C: its slots static). measured on config 5's IQ2_XXS gate (us): 1 block ahead
-  // 1239, 2 1146, 4 1195
-  constexpr int PD = C >= 2 ? 2 : 1;
+  static_assert(G >= 2, "one group a pass: kernel16");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
   if (!n) return;  // (the whole workgroup)
@@ -283,152 +283,69 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
   for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
     __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
     const int groups = (int) ((n - c0 + kGroup - 1) / kGroup) < G ? (int) ((n - c0 + kGroup - 1) / kGroup) : G;
-    uint32_t voff[G], xoff[G];
+    uint32_t voff[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
       const uint32_t t = c0 + g * kGroup + col / 2;
       voff[g] = lives && t < n ? t * cols + 8 * quad : 0x80000000u;
-      const uint32_t to = c0 + g * kGroup + ot + (col & 1);
-      xoff[g] = to < n ? to * nblk * 4 : 0x80000000u;
     }
     float acc[C][G][2];
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
       for (int g = 0; g < G; g++) acc[c][g][0] = acc[c][g][1] = 0.0f;
-    if constexpr (G == 1) {
-      // the A words of the wave's blocks, PD blocks ahead (a ring of PD register sets: the loads' latency is the
-      // kernel's bound, not its arithmetic). every load is made, on every path (a zero of the layout, or a group past
-      // the count, at an offset past the descriptor's end: zeros, no access), so the loads in flight are counted
-      // exactly and each wait is for the oldest alone
-      long an[PD][G];
-      auto aload = [&](int slot, uint32_t s) __attribute__((always_inline)) {
-  #pragma unroll
-        for (int g = 0; g < G; g++)
-          an[slot][g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
-      };
-      // the token scales of a round's C blocks (s0 + W c), one load a lane a round: lane col of a 16-lane row holds
-      // token ot + (col & 1)'s scale of block s0 + W (col / 2) (col / 2 < C), and each block's two broadcast from it
-      const uint32_t kc = (uint32_t) (col / 2) < (uint32_t) C ? (uint32_t) (col / 2) : (uint32_t) (C - 1);
-      // (the first round's scales first, then the ring: in the order every round issues them, scales before A words)
-      float sn[G];
-      {
-        const uint32_t sb = wave + W * kc < nblk ? wave + W * kc : nblk - 1;  // (per lane: a vector offset)
-  #pragma unroll
-        for (int g = 0; g < G; g++)
-          sn[g] = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff[g] == 0x80000000u ? xoff[g] : xoff[g] + sb * 4, 0, 0));
+    // two or more groups a pass (the types whose decode is dearest: each decoded block serves both): the A words and
+    // token scales one block ahead, each lane loading its two outputs' scales (a ring here costs these kernels
+    // their occupancy)
+    uint32_t xo[G][2];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+      for (int p = 0; p < 2; p++) {
+        const uint32_t to = c0 + g * kGroup + ot + p;
+        xo[g][p] = to < n ? to * nblk * 4 : 0x80000000u;
       }
-      __builtin_amdgcn_sched_barrier(0);  // (kept in that order, the ring in slot order)
-  #pragma unroll
-      for (int i = 0; i < PD; i++) {
-        aload(i, wave + W * i < nblk ? wave + W * i : nblk - 1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // (no value is copied from round to round: each ring slot is reloaded only after the MFMA that reads it, and the
-      // rounds take their scales from two register sets in turn, each round loading the next round's into the other -
-      // a loop-carried copy would wait for its load, and with it every load made since)
-      float sa[G], sb2[G];
-  #pragma unroll
-      for (int g = 0; g < G; g++) sa[g] = sn[g];
-      auto round = [&](uint32_t s0, float (&sc)[G], float (&nx_sc)[G]) __attribute__((always_inline)) {
-        {
-          const uint32_t nx = s0 + L < nblk ? s0 + L : s0;  // (the next round's, a round ahead)
-          const uint32_t sb = nx + W * kc < nblk ? nx + W * kc : nblk - 1;
-  #pragma unroll
-          for (int g = 0; g < G; g++)
-            nx_sc[g] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff[g] == 0x80000000u ? xoff[g] : xoff[g] + sb * 4, 0, 0));
-        }
-  #pragma unroll
-        for (int c = 0; c < C; c++) {
-          const uint32_t s = s0 + W * c;  // logical lane wave + W c
-          if (!FULL && s >= nblk) break;  // (uniform; FULL: every round whole)
-          const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
-          const int j = (int) (s % per);
-          uint32_t w0, w1;
-          chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
-          const long b = (long) (((uint64_t) w1 << 32) | w0);
-          float f0, f1;
-          factors<T>((lbytes) blk, j, f0, f1);
-          const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
-          v4i D[G];
-  #pragma unroll
-          for (int g = 0; g < G; g++)
-            if (g < groups) D[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD][g], b, bias, 0, 0, 0);
-          aload(c % PD, s + W * PD < nblk ? s + W * PD : s);  // (past the last block: loaded again, unused - no branch)
-  #pragma unroll
-          for (int g = 0; g < G; g++) {
-            if (g < groups) {
-              const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[g][0]), n0),
-                                          __builtin_fmaf(f1, __int_as_float(D[g][1]), n1));
-              const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[g][2]), n0),
-                                          __builtin_fmaf(f1, __int_as_float(D[g][3]), n1));
-              acc[c][g][0] = __builtin_fmaf(row_bcast(sc[g], 2 * c), s0_, acc[c][g][0]);
-              acc[c][g][1] = __builtin_fmaf(row_bcast(sc[g], 2 * c + 1), s1_, acc[c][g][1]);
-            }
-          }
-        }
-      };
-      for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += 2 * L) {
-        round(s0, sa, sb2);
-        if (s0 + L >= nblk) break;
-        round(s0 + L, sb2, sa);
-      }
-    } else {
-      // two or more groups a pass (the types whose decode is dearest: each decoded block serves both): the A words and
-      // token scales one block ahead, each lane loading its two outputs' scales (a ring here costs these kernels
-      // their occupancy)
-      uint32_t xo[G][2];
+    long an[G];
+    float xn[G][2];
+    auto aload = [&](uint32_t s) __attribute__((always_inline)) {
 #pragma unroll
       for (int g = 0; g < G; g++)
+        if (g < groups) {
+          an[g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
 #pragma unroll
-        for (int p = 0; p < 2; p++) {
-          const uint32_t to = c0 + g * kGroup + ot + p;
-          xo[g][p] = to < n ? to * nblk * 4 : 0x80000000u;
+          for (int p = 0; p < 2; p++)
+            xn[g][p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(dr, xo[g][p], s * 4, 0));
         }
-      long an[G];
-      float xn[G][2];
-      auto aload = [&](uint32_t s) __attribute__((always_inline)) {
+    };
+    aload((uint32_t) wave);
+    for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += L) {
 #pragma unroll
-        for (int g = 0; g < G; g++)
+      for (int c = 0; c < C; c++) {
+        const uint32_t s = s0 + W * c;  // logical lane wave + W c
+        if (!FULL && s >= nblk) break;  // (uniform)
+        long a[G];
+        float x[G][2];
+#pragma unroll
+        for (int g = 0; g < G; g++) a[g] = an[g], x[g][0] = xn[g][0], x[g][1] = xn[g][1];
+        aload(s + W < nblk ? s + W : s);  // (the last block: loaded again, unused - no branch)
+        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+        const int j = (int) (s % per);
+        uint32_t w0, w1;
+        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+        const long b = (long) (((uint64_t) w1 << 32) | w0);
+        float f0, f1;
+        factors<T>((lbytes) blk, j, f0, f1);
+        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
           if (g < groups) {
-            an[g] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff[g], s * 32, 0));
-#pragma unroll
-            for (int p = 0; p < 2; p++)
-              xn[g][p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(dr, xo[g][p], s * 4, 0));
-          }
-      };
-      aload((uint32_t) wave);
-      for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += L) {
-#pragma unroll
-        for (int c = 0; c < C; c++) {
-          const uint32_t s = s0 + W * c;  // logical lane wave + W c
-          if (!FULL && s >= nblk) break;  // (uniform)
-          long a[G];
-          float x[G][2];
-#pragma unroll
-          for (int g = 0; g < G; g++) a[g] = an[g], x[g][0] = xn[g][0], x[g][1] = xn[g][1];
-          aload(s + W < nblk ? s + W : s);  // (the last block: loaded again, unused - no branch)
-          const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
-          const int j = (int) (s % per);
-          uint32_t w0, w1;
-          chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
-          const long b = (long) (((uint64_t) w1 << 32) | w0);
-          float f0, f1;
-          factors<T>((lbytes) blk, j, f0, f1);
-          const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
-#pragma unroll
-          for (int g = 0; g < G; g++) {
-            if (g < groups) {
-              const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[g], b, bias, 0, 0, 0);
-              const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0),
-                                          __builtin_fmaf(f1, __int_as_float(D[1]), n1));
-              const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0),
-                                          __builtin_fmaf(f1, __int_as_float(D[3]), n1));
-              acc[c][g][0] = __builtin_fmaf(x[g][0], s0_, acc[c][g][0]);
-              acc[c][g][1] = __builtin_fmaf(x[g][1], s1_, acc[c][g][1]);
-            }
+            const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[g], b, bias, 0, 0, 0);
+            const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0),
+                                        __builtin_fmaf(f1, __int_as_float(D[1]), n1));
+            const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0),
+                                        __builtin_fmaf(f1, __int_as_float(D[3]), n1));
+            acc[c][g][0] = __builtin_fmaf(x[g][0], s0_, acc[c][g][0]);
+            acc[c][g][1] = __builtin_fmaf(x[g][1], s1_, acc[c][g][1]);
           }
         }
       }
@@ -469,12 +386,147 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
   }
 }
 
+// one group of 16 tokens a pass, the halves split on the weights' side: the A operand's 16 rows are 16 tokens (lane l:
+// token l % 16's values 8 (l / 16) .. + 7 of the block - every lane a token's bytes, none a zero of the layout), and two
+// MFMAs take the block's B words with the second half's k zeroed and with the first half's: lane l holds the two
+// half-dots of tokens 4 (l / 16) + i, i < 4, for its weight row l % 16. the same products, sums and chains as kernel's
+// (one A load a block serves 16 tokens, not 8: the kernel is bound by its loads). the token scales: lane col of a
+// 16-lane row loads token 4 (row) + col % 4's scale of the round's block col / 4, each block's four broadcast from it
+template <uint32_t T, int L, int W, bool FULL>
+__global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __restrict__ w,
+                                                     const int32_t* __restrict__ cnt, const int32_t* __restrict__ xrow,
+                                                     uint32_t cols, const int8_t* __restrict__ q,
+                                                     const float* __restrict__ d, float* __restrict__ y, uint32_t ys) {
+  constexpr int kThreads = W * kWave, per = (int) (Block<T>::values / 32), C = L / W, TOK = 16;
+  // the A ring's depth (a divisor of C: its slots static). measured on config 5's IQ2_XXS gate with 8 tokens a group
+  // (us): 1 block ahead 1239, 2 1146, 4 1195
+  constexpr int PD = C >= 2 ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t m = blockIdx.y, n = (uint32_t) cnt[m];
+  if (!n) return;  // (the whole workgroup)
+  const int wave = __builtin_amdgcn_readfirstlane((int) (threadIdx.x / kWave)), lane = threadIdx.x % kWave;
+  const int col = lane % 16, quad = lane / 16;
+  const uint32_t row0 = blockIdx.x * kTile, nblk = cols / 32, r0 = (uint32_t) xrow[m];
+  const uint32_t rb = (uint32_t) row_bytes<T>(cols);
+  const Lds<1, W> L_(rb, grid_bytes_of<T>());
+  {  // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
+    const u32x4* src = (const u32x4*) (table_at(w, m) + (uint64_t) row0 * rb);
+    const uint32_t nw = 16 * rb / 16;
+    for (uint32_t i = threadIdx.x; i < nw; i += kThreads) ((u32x4*) (smem + L_.slab))[i] = src[i];
+    constexpr uint32_t ng = grid_bytes_of<T>() / 16;
+    const u32x4* gs = (const u32x4*) const_grid<T>();
+    for (uint32_t i = threadIdx.x; i < ng; i += kThreads) ((u32x4*) (smem + L_.grid))[i] = gs[i];
+    if (threadIdx.x < 128) ((uint64_t*) (smem + L_.sm))[threadIdx.x] = sign_mask(threadIdx.x);
+  }
+  const auto* grid = (const typename GridOf<T>::E*) (smem + L_.grid);
+  const uint64_t* sm = (const uint64_t*) (smem + L_.sm);
+  float* part = (float*) (smem + L_.part);  // [wave][pair][lane]: two outputs a lane at a time
+  const uint8_t* brow = smem + L_.slab + col * rb;  // this lane's B row (a weight row)
+  const __amdgpu_buffer_rsrc_t qr =
+      __builtin_amdgcn_make_buffer_rsrc((void*) (q + (uint64_t) r0 * cols), (short) 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t dr =
+      __builtin_amdgcn_make_buffer_rsrc((void*) (d + (uint64_t) r0 * nblk), (short) 0, 0x7FFFFFFF, 0x00020000);
+  const uint32_t kc = (uint32_t) (col / 4) < (uint32_t) C ? (uint32_t) (col / 4) : (uint32_t) (C - 1);
+  v4i bias = {kBias, kBias, kBias, kBias};
+  asm volatile("" : "+v"(bias));  // (held in registers, not rebuilt before every MFMA)
+  for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
+    __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
+    // every load made on every path (a token past the count at an offset past the descriptor's end: zeros, no access)
+    const uint32_t voff = c0 + col < n ? (c0 + col) * cols + 8 * quad : 0x80000000u;
+    const uint32_t to = c0 + 4 * quad + (col & 3);
+    const uint32_t xoff = to < n ? to * nblk * 4 : 0x80000000u;
+    float acc[C][4];
+#pragma unroll
+    for (int c = 0; c < C; c++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[c][i] = 0.0f;
+    long an[PD];
+    auto aload = [&](int slot, uint32_t s) __attribute__((always_inline)) {
+      an[slot] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff, s * 32, 0));
+    };
+    auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
+      const uint32_t sb = s0 + W * kc < nblk ? s0 + W * kc : nblk - 1;  // (per lane: a vector offset)
+      return __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff == 0x80000000u ? xoff : xoff + sb * 4, 0, 0));
+    };
+    // (the first round's scales, then the ring in slot order: the order every round issues them)
+    float sa = sload((uint32_t) wave), sb2;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PD; i++) {
+      aload(i, wave + W * i < nblk ? wave + W * i : nblk - 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    auto round = [&](uint32_t s0, float& sc, float& nx_sc) __attribute__((always_inline)) {
+      nx_sc = sload(s0 + L < nblk ? s0 + L : s0);  // (the next round's, a round ahead, into the other register)
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const uint32_t s = s0 + W * c;  // logical lane wave + W c
+        if (!FULL && s >= nblk) break;  // (uniform; FULL: every round whole)
+        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+        const int j = (int) (s % per);
+        uint32_t w0, w1;
+        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+        const long b = (long) (((uint64_t) w1 << 32) | w0);
+        const long blo = quad < 2 ? b : 0, bhi = quad < 2 ? 0 : b;  // (k 0 .. 15: the first half, 16 .. 31 the second)
+        float f0, f1;
+        factors<T>((lbytes) blk, j, f0, f1);
+        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+        const v4i Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], blo, bias, 0, 0, 0);
+        const v4i Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], bhi, bias, 0, 0, 0);
+        aload(c % PD, s + W * PD < nblk ? s + W * PD : s);  // (past the last block: loaded again, unused)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float s_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(Dl[i]), n0),
+                                     __builtin_fmaf(f1, __int_as_float(Dh[i]), n1));
+          acc[c][i] = __builtin_fmaf(row_bcast(sc, 4 * c + i), s_, acc[c][i]);
+        }
+      }
+    };
+    for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += 2 * L) {
+      round(s0, sa, sb2);
+      if (s0 + L >= nblk) break;
+      round(s0 + L, sb2, sa);
+    }
+    // the tree's levels L/2 .. W within the wave: chains c and c + o (logical lanes ll and ll ^ W o)
+#pragma unroll
+    for (int o = C / 2; o > 0; o >>= 1)
+#pragma unroll
+      for (int c = 0; c < o; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[c][i] = __fadd_rn(acc[c][i], acc[c + o][i]);
+    // levels W/2 .. 1 across the waves through LDS, two of the lane's four outputs at a time
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+      if (hh) __syncthreads();  // (the first pair read)
+#pragma unroll
+      for (int p = 0; p < 2; p++) part[(wave * 2 + p) * kWave + lane] = acc[0][2 * hh + p];
+      __syncthreads();
+      for (int p = (int) wave; p < 2; p += W) {
+        float t[W];
+#pragma unroll
+        for (int v = 0; v < W; v++) t[v] = part[(v * 2 + p) * kWave + lane];
+#pragma unroll
+        for (int o = W / 2; o > 0; o >>= 1)
+#pragma unroll
+          for (int v = 0; v < o; v++) t[v] = __fadd_rn(t[v], t[v + o]);
+        const uint32_t tk = c0 + 4 * quad + 2 * hh + p;
+        if (tk < n) y[(uint64_t) (r0 + tk) * ys + row0 + col] = t[0];
+      }
+    }
+  }
+}
+
 template <uint32_t T, int L, int G, int W>
 bool launch(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t rows,
             uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
   const Lds<G, W> l((uint32_t) row_bytes<T>(cols), grid_bytes_of<T>());
   if (l.total > 160 * 1024) return false;
-  auto k = (cols / 32) % L == 0 ? kernel<T, L, G, W, true> : kernel<T, L, G, W, false>;
+  auto pick = [&]() {
+    if constexpr (G == 1) return (cols / 32) % L == 0 ? kernel16<T, L, W, true> : kernel16<T, L, W, false>;
+    else return (cols / 32) % L == 0 ? kernel<T, L, G, W, true> : kernel<T, L, G, W, false>;
+  };
+  auto k = pick();
   if (l.total > 64 * 1024 &&
       hipFuncSetAttribute((const void*) k, hipFuncAttributeMaxDynamicSharedMemorySize, (int) l.total) != hipSuccess)
     return false;
