@@ -391,7 +391,9 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
 // MFMAs take the block's B words with the second half's k zeroed and with the first half's: lane l holds the two
 // half-dots of tokens 4 (l / 16) + i, i < 4, for its weight row l % 16. the same products, sums and chains as kernel's
 // (one A load a block serves 16 tokens, not 8: the kernel is bound by its loads). the token scales: lane col of a
-// 16-lane row loads token 4 (row) + col % 4's scale of the round's block col / 4, each block's four broadcast from it
+// 16-lane row loads token 4 (row) + col % 4's scale of the round's block col / 4, each block's four broadcast from it.
+// a matrix's last pass with at most 8 tokens takes the 8-token layout instead (pass8: one MFMA a block, 2 outputs a
+// lane, all live; config 5's IQ2_XXS gate 1095-1119 -> 1049-1072 us, the same bits)
 template <uint32_t T, int L, int W, bool FULL>
 __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __restrict__ w,
                                                      const int32_t* __restrict__ cnt, const int32_t* __restrict__ xrow,
@@ -429,8 +431,88 @@ __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __re
   const uint32_t kc = (uint32_t) (col / 4) < (uint32_t) C ? (uint32_t) (col / 4) : (uint32_t) (C - 1);
   v4i bias = {kBias, kBias, kBias, kBias};
   asm volatile("" : "+v"(bias));  // (held in registers, not rebuilt before every MFMA)
+  // a pass of at most 8 tokens: the A operand's 16 rows are its 8 tokens' halves (row i: token i / 2's half i % 2,
+  // the other half's k zeros of the layout), so one MFMA gives both half-dots of the 8 tokens and lane l holds both
+  // halves of tokens 2 (l / 16), 2 (l / 16) + 1 for its row: half the epilogue of a 16-token pass, every output live
+  auto pass8 = [&](uint32_t c0) __attribute__((always_inline)) {
+    const bool lives = (col % 2 == 0) == (quad < 2);
+    const uint32_t t = c0 + col / 2, to = c0 + 2 * quad + (col & 1);
+    const uint32_t voff = lives && t < n ? t * cols + 8 * quad : 0x80000000u;
+    const uint32_t xoff = to < n ? to * nblk * 4 : 0x80000000u;
+    const uint32_t kc8 = (uint32_t) (col / 2) < (uint32_t) C ? (uint32_t) (col / 2) : (uint32_t) (C - 1);
+    float acc[C][2];
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[c][0] = acc[c][1] = 0.0f;
+    long an[PD];
+    auto aload = [&](int slot, uint32_t s) __attribute__((always_inline)) {
+      an[slot] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff, s * 32, 0));
+    };
+    auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
+      const uint32_t sb = s0 + W * kc8 < nblk ? s0 + W * kc8 : nblk - 1;
+      return __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff == 0x80000000u ? xoff : xoff + sb * 4, 0, 0));
+    };
+    float sa = sload((uint32_t) wave), sb2;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PD; i++) {
+      aload(i, wave + W * i < nblk ? wave + W * i : nblk - 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    auto round = [&](uint32_t s0, float& sc, float& nx_sc) __attribute__((always_inline)) {
+      nx_sc = sload(s0 + L < nblk ? s0 + L : s0);
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const uint32_t s = s0 + W * c;
+        if (!FULL && s >= nblk) break;  // (uniform)
+        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+        const int j = (int) (s % per);
+        uint32_t w0, w1;
+        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+        const long b = (long) (((uint64_t) w1 << 32) | w0);
+        float f0, f1;
+        factors<T>((lbytes) blk, j, f0, f1);
+        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+        const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], b, bias, 0, 0, 0);
+        aload(c % PD, s + W * PD < nblk ? s + W * PD : s);
+        const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0), __builtin_fmaf(f1, __int_as_float(D[1]), n1));
+        const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0), __builtin_fmaf(f1, __int_as_float(D[3]), n1));
+        acc[c][0] = __builtin_fmaf(row_bcast(sc, 2 * c), s0_, acc[c][0]);
+        acc[c][1] = __builtin_fmaf(row_bcast(sc, 2 * c + 1), s1_, acc[c][1]);
+      }
+    };
+    for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += 2 * L) {
+      round(s0, sa, sb2);
+      if (s0 + L >= nblk) break;
+      round(s0 + L, sb2, sa);
+    }
+#pragma unroll
+    for (int o = C / 2; o > 0; o >>= 1)
+#pragma unroll
+      for (int c = 0; c < o; c++)
+#pragma unroll
+        for (int p = 0; p < 2; p++) acc[c][p] = __fadd_rn(acc[c][p], acc[c + o][p]);
+#pragma unroll
+    for (int p = 0; p < 2; p++) part[(wave * 2 + p) * kWave + lane] = acc[0][p];
+    __syncthreads();
+    for (int p = (int) wave; p < 2; p += W) {
+      float tv[W];
+#pragma unroll
+      for (int v = 0; v < W; v++) tv[v] = part[(v * 2 + p) * kWave + lane];
+#pragma unroll
+      for (int o = W / 2; o > 0; o >>= 1)
+#pragma unroll
+        for (int v = 0; v < o; v++) tv[v] = __fadd_rn(tv[v], tv[v + o]);
+      const uint32_t tk = c0 + 2 * quad + p;
+      if (tk < n) y[(uint64_t) (r0 + tk) * ys + row0 + col] = tv[0];
+    }
+  };
   for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
     __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
+    if (n - c0 <= 8) {  // (uniform)
+      pass8(c0);
+      continue;
+    }
     // every load made on every path (a token past the count at an offset past the descriptor's end: zeros, no access)
     const uint32_t voff = c0 + col < n ? (c0 + col) * cols + 8 * quad : 0x80000000u;
     const uint32_t to = c0 + 4 * quad + (col & 3);

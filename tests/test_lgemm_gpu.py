@@ -36,7 +36,7 @@ def run(g, t, ws, counts, rows, cols, q, d):
 def test_lane_group_oracle(g, name, cols):
     t = synth.ID[name]
     rows = 80  # a workgroup's 64 rows and a partial one
-    counts = [1, 17, 40, 5]
+    counts = [1, 17, 40, 5, 29]  # (last passes of 1, 1, 8, 5 tokens: the 8-token layout; 29: 16 + 13)
     ws = [synth.iq_blocks(t, rows, cols, 70 + m) for m in range(len(counts))]
     rng = np.random.default_rng(cols + t)
     x = rng.normal(0, 1, (int(np.sum(counts)), cols)).astype(np.float32)
