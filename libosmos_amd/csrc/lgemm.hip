@@ -198,7 +198,9 @@ constexpr int kGroup = 8;
 // kernels are bound by their loads, not their decode (a build of kernel without the decode ran 1227 us against 1241,
 // one without its A loads 890): kernel16 halves the A loads a full group issues. measured on config 5's routing (512
 // tokens, 250 experts, the busiest 441), us, 2048 x 7168 / 7168 x 2048: kernel16 (W 8 / 4) IQ2_XXS 1098 / 1201,
-// IQ1_S 1133 / 1283, IQ2_XS 1136 / 1260, IQ2_S 1399 / 1434, IQ3_XXS 1260 (W 16; 1326 at 8) / 1421; kernel with one group
+// IQ1_S 1133 / 1283, IQ2_XS 1136 / 1260, IQ2_S 1399 / 1434, IQ3_XXS 1260 (W 16; 1326 at 8) / 1421, and with the
+// last pass of at most 8 tokens in the 8-token layout 1055 / 1189, 1064 / 1232, 1082 / 1217, 1340 / -, 1218 / 1376;
+// kernel with one group
 // of 8 a pass 1161 / 1223, 1188 / 1325, 1214 / 1254, 1583 / 1497, 1612 / 1508 (it was 1308 / 1362 for IQ2_XXS before
 // its loads were reworked); with two groups 1344 / 1360, 1347 / 1509, 1368 / 1386, 1709 / 1501, 1411 (W 16) / 1747;
 // IQ1_M two groups 1426 / 2107 against kernel16's 1450 / 2113 and one group's 2015 / 3169 (its scale decode holds 88
@@ -434,6 +436,8 @@ __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __re
   // a pass of at most 8 tokens: the A operand's 16 rows are its 8 tokens' halves (row i: token i / 2's half i % 2,
   // the other half's k zeros of the layout), so one MFMA gives both half-dots of the 8 tokens and lane l holds both
   // halves of tokens 2 (l / 16), 2 (l / 16) + 1 for its row: half the epilogue of a 16-token pass, every output live
+  // (not IQ2_S at 16 lanes: its registers would cross 96, one wave a SIMD fewer - 1434 -> 1472 us at 7168 x 2048)
+  constexpr bool kPass8 = !(T == kIQ2_S && L == 16);
   auto pass8 = [&](uint32_t c0) __attribute__((always_inline)) {
     const bool lives = (col % 2 == 0) == (quad < 2);
     const uint32_t t = c0 + col / 2, to = c0 + 2 * quad + (col & 1);
@@ -509,9 +513,11 @@ __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __re
   };
   for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
     __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
-    if (n - c0 <= 8) {  // (uniform)
-      pass8(c0);
-      continue;
+    if constexpr (kPass8) {
+      if (n - c0 <= 8) {  // (uniform)
+        pass8(c0);
+        continue;
+      }
     }
     // every load made on every path (a token past the count at an offset past the descriptor's end: zeros, no access)
     const uint32_t voff = c0 + col < n ? (c0 + col) * cols + 8 * quad : 0x80000000u;
