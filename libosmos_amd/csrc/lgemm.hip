@@ -225,7 +225,7 @@ constexpr uint32_t grid_bytes_of() {
 }
 
 // dynamic LDS: the workgroup's 16 weight rows (the whole slab), the codebook, the sign masks, the waves' partial trees
-template <int G, int W>
+template <int G, int W, int L = 0>
 struct Lds {
   uint32_t slab, grid, sm, part, total;
   __host__ __device__ Lds(uint32_t rb, uint32_t grid_bytes) {
@@ -233,9 +233,21 @@ struct Lds {
     grid = (16 * rb + 15) / 16 * 16;
     sm = grid + grid_bytes;
     part = sm + 128 * 8;
-    total = part + W * G * 2 * kWave * 4;
+    // (L: kernel16 staging a round's A rows, 16 tokens x L blocks, kAS = 32 L + 16 bytes apart, where the partial
+    // trees go at the pass's end)
+    const uint32_t tree = W * G * 2 * kWave * 4, arow = L ? 16 * (32 * L + 16) : 0;
+    total = part + (tree > arow ? tree : arow);
   }
 };
+// kernel16 with each round's A rows staged in LDS (16-byte loads of the 16 tokens' bytes, the next round's in registers
+// meanwhile) rather than loaded a lane's 8 bytes at a time: measured on config 5's routing, us, 2048 x 7168 (32
+// lanes) / 7168 x 2048 (16 lanes), staged against not: IQ2_XXS 953 (held to 6 waves a SIMD: 80 VGPRs, 7 spilled;
+// 1078 without) / 1010 against 1053 / 1192, IQ1_S 1149 / 1163 against 1065 / 1232, IQ2_XS 1140 / 1046 against
+// 1084 / 1219, IQ2_S 1410 / 1574 against 1339 / 1434, IQ3_XXS 1690 / 1320 against 1218 / 1375
+template <uint32_t T, int L>
+constexpr bool stage_a() {
+  return T != kIQ2_S && (L == 16 || T == kIQ2_XXS);
+}
 
 // blockIdx.x: 16 rows; blockIdx.y: the matrix, its cnt[m] tokens from row xrow[m] of q / d, G groups of 8 a pass.
 // wave w takes the blocks s = w (mod W): its chains are the logical lanes ll = w (mod W), L / W accumulators an
@@ -397,7 +409,9 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
 // a matrix's last pass with at most 8 tokens takes the 8-token layout instead (pass8: one MFMA a block, 2 outputs a
 // lane, all live; config 5's IQ2_XXS gate 1095-1119 -> 1049-1072 us, the same bits)
 template <uint32_t T, int L, int W, bool FULL>
-__global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __restrict__ w,
+// (IQ2_XXS at 32 lanes with whole rounds held to 80 VGPRs, 6 waves a SIMD: 1078 -> 953 us, 7 registers spilled)
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(T == kIQ2_XXS && L == 32 && FULL ? 6 : 1)))
+void kernel16(const uint8_t* const* __restrict__ w,
                                                      const int32_t* __restrict__ cnt, const int32_t* __restrict__ xrow,
                                                      uint32_t cols, const int8_t* __restrict__ q,
                                                      const float* __restrict__ d, float* __restrict__ y, uint32_t ys) {
@@ -412,7 +426,8 @@ __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __re
   const int col = lane % 16, quad = lane / 16;
   const uint32_t row0 = blockIdx.x * kTile, nblk = cols / 32, r0 = (uint32_t) xrow[m];
   const uint32_t rb = (uint32_t) row_bytes<T>(cols);
-  const Lds<1, W> L_(rb, grid_bytes_of<T>());
+  constexpr bool kStageA = stage_a<T, L>();
+  const Lds<1, W, kStageA ? L : 0> L_(rb, grid_bytes_of<T>());
   {  // the slab (16 rows x rb: contiguous, 16-aligned) and the codebook into LDS
     const u32x4* src = (const u32x4*) (table_at(w, m) + (uint64_t) row0 * rb);
     const uint32_t nw = 16 * rb / 16;
@@ -519,62 +534,132 @@ __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __re
         continue;
       }
     }
-    // every load made on every path (a token past the count at an offset past the descriptor's end: zeros, no access)
-    const uint32_t voff = c0 + col < n ? (c0 + col) * cols + 8 * quad : 0x80000000u;
-    const uint32_t to = c0 + 4 * quad + (col & 3);
-    const uint32_t xoff = to < n ? to * nblk * 4 : 0x80000000u;
     float acc[C][4];
 #pragma unroll
     for (int c = 0; c < C; c++)
 #pragma unroll
       for (int i = 0; i < 4; i++) acc[c][i] = 0.0f;
-    long an[PD];
-    auto aload = [&](int slot, uint32_t s) __attribute__((always_inline)) {
-      an[slot] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff, s * 32, 0));
-    };
-    auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
-      const uint32_t sb = s0 + W * kc < nblk ? s0 + W * kc : nblk - 1;  // (per lane: a vector offset)
-      return __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff == 0x80000000u ? xoff : xoff + sb * 4, 0, 0));
-    };
-    // (the first round's scales, then the ring in slot order: the order every round issues them)
-    float sa = sload((uint32_t) wave), sb2;
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kStageA) {
+      // the round's A bytes (the pass's 16 tokens x L blocks x 32 bytes) staged in LDS by the whole workgroup with
+      // 16-byte loads, the next round's in registers meanwhile; row t of the buffer token c0 + t's, kAS bytes apart
+      const uint32_t to = c0 + 4 * quad + (col & 3);
+      const uint32_t xoff = to < n ? to * nblk * 4 : 0x80000000u;
+      constexpr int PW = C / 2;  // 16-byte words a thread stages a round: 16 x 2L words over W waves
+      static_assert(C % 2 == 0, "whole words a thread");
+      constexpr uint32_t kAS = 32 * L + 16;
+      uint8_t* abuf = smem + L_.part;
+      uint32_t gof[PW], lof[PW];
 #pragma unroll
-    for (int i = 0; i < PD; i++) {
-      aload(i, wave + W * i < nblk ? wave + W * i : nblk - 1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    auto round = [&](uint32_t s0, float& sc, float& nx_sc) __attribute__((always_inline)) {
-      nx_sc = sload(s0 + L < nblk ? s0 + L : s0);  // (the next round's, a round ahead, into the other register)
-#pragma unroll
-      for (int c = 0; c < C; c++) {
-        const uint32_t s = s0 + W * c;  // logical lane wave + W c
-        if (!FULL && s >= nblk) break;  // (uniform; FULL: every round whole)
-        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
-        const int j = (int) (s % per);
-        uint32_t w0, w1;
-        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
-        const long b = (long) (((uint64_t) w1 << 32) | w0);
-        const long blo = quad < 2 ? b : 0, bhi = quad < 2 ? 0 : b;  // (k 0 .. 15: the first half, 16 .. 31 the second)
-        float f0, f1;
-        factors<T>((lbytes) blk, j, f0, f1);
-        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
-        const v4i Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], blo, bias, 0, 0, 0);
-        const v4i Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], bhi, bias, 0, 0, 0);
-        aload(c % PD, s + W * PD < nblk ? s + W * PD : s);  // (past the last block: loaded again, unused)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float s_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(Dl[i]), n0),
-                                     __builtin_fmaf(f1, __int_as_float(Dh[i]), n1));
-          acc[c][i] = __builtin_fmaf(row_bcast(sc, 4 * c + i), s_, acc[c][i]);
-        }
+      for (int u = 0; u < PW; u++) {
+        const uint32_t wi = threadIdx.x + u * kThreads, tk = wi / (2 * L), o16 = wi % (2 * L);
+        gof[u] = c0 + tk < n ? (c0 + tk) * cols + o16 * 16 : 0x80000000u;
+        lof[u] = tk * kAS + o16 * 16;
       }
-    };
-    for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += 2 * L) {
-      round(s0, sa, sb2);
-      if (s0 + L >= nblk) break;
-      round(s0 + L, sb2, sa);
+      u32x4 st[PW];
+      auto gstage = [&](uint32_t b0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < PW; u++)
+          st[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, gof[u], b0 * 32, 0));
+      };
+      auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
+        const uint32_t sb = s0 + W * kc < nblk ? s0 + W * kc : nblk - 1;  // (per lane: a vector offset)
+        return __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff == 0x80000000u ? xoff : xoff + sb * 4, 0, 0));
+      };
+      const uint32_t nr = (nblk + L - 1) / L;
+      gstage(0);
+      float sa = sload((uint32_t) wave), sb2;
+      auto round = [&](uint32_t r, float& sc, float& nx_sc) __attribute__((always_inline)) {
+        __syncthreads();  // (the round before read by every wave)
+#pragma unroll
+        for (int u = 0; u < PW; u++) *(u32x4*) (abuf + lof[u]) = st[u];
+        __syncthreads();
+        gstage(r + 1 < nr ? (r + 1) * L : r * L);  // (past the last round: the last again, unused)
+        const uint32_t s0 = r * L + wave;
+        nx_sc = sload(s0 + L < nblk ? s0 + L : s0);
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          const uint32_t s = s0 + W * c;  // logical lane wave + W c
+          if (!FULL && s >= nblk) break;  // (uniform in the wave)
+          const long a = *(const long*) (abuf + col * kAS + (wave + W * c) * 32 + 8 * quad);
+          const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+          const int j = (int) (s % per);
+          uint32_t w0, w1;
+          chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+          const long b = (long) (((uint64_t) w1 << 32) | w0);
+          const long blo = quad < 2 ? b : 0, bhi = quad < 2 ? 0 : b;  // (k 0 .. 15: the first half, 16 .. 31 the second)
+          float f0, f1;
+          factors<T>((lbytes) blk, j, f0, f1);
+          const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+          const v4i Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, blo, bias, 0, 0, 0);
+          const v4i Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bhi, bias, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float s_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(Dl[i]), n0),
+                                       __builtin_fmaf(f1, __int_as_float(Dh[i]), n1));
+            acc[c][i] = __builtin_fmaf(row_bcast(sc, 4 * c + i), s_, acc[c][i]);
+          }
+        }
+      };
+      for (uint32_t r = 0; r < nr; r += 2) {  // (uniform: every wave meets every barrier)
+        round(r, sa, sb2);
+        if (r + 1 >= nr) break;
+        round(r + 1, sb2, sa);
+      }
+      __syncthreads();  // (the last round's A rows read: the partial trees go where they were)
+    } else {
+      // every load made on every path (a token past the count at an offset past the descriptor's end: zeros, no access)
+      const uint32_t voff = c0 + col < n ? (c0 + col) * cols + 8 * quad : 0x80000000u;
+      const uint32_t to = c0 + 4 * quad + (col & 3);
+      const uint32_t xoff = to < n ? to * nblk * 4 : 0x80000000u;
+      long an[PD];
+      auto aload = [&](int slot, uint32_t s) __attribute__((always_inline)) {
+        an[slot] = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(qr, voff, s * 32, 0));
+      };
+      auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
+        const uint32_t sb = s0 + W * kc < nblk ? s0 + W * kc : nblk - 1;  // (per lane: a vector offset)
+        return __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff == 0x80000000u ? xoff : xoff + sb * 4, 0, 0));
+      };
+      // (the first round's scales, then the ring in slot order: the order every round issues them)
+      float sa = sload((uint32_t) wave), sb2;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < PD; i++) {
+        aload(i, wave + W * i < nblk ? wave + W * i : nblk - 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      auto round = [&](uint32_t s0, float& sc, float& nx_sc) __attribute__((always_inline)) {
+        nx_sc = sload(s0 + L < nblk ? s0 + L : s0);  // (the next round's, a round ahead, into the other register)
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+          const uint32_t s = s0 + W * c;  // logical lane wave + W c
+          if (!FULL && s >= nblk) break;  // (uniform; FULL: every round whole)
+          const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+          const int j = (int) (s % per);
+          uint32_t w0, w1;
+          chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+          const long b = (long) (((uint64_t) w1 << 32) | w0);
+          const long blo = quad < 2 ? b : 0, bhi = quad < 2 ? 0 : b;  // (k 0 .. 15: the first half, 16 .. 31 the second)
+          float f0, f1;
+          factors<T>((lbytes) blk, j, f0, f1);
+          const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+          const v4i Dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], blo, bias, 0, 0, 0);
+          const v4i Dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[c % PD], bhi, bias, 0, 0, 0);
+          aload(c % PD, s + W * PD < nblk ? s + W * PD : s);  // (past the last block: loaded again, unused)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float s_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(Dl[i]), n0),
+                                       __builtin_fmaf(f1, __int_as_float(Dh[i]), n1));
+            acc[c][i] = __builtin_fmaf(row_bcast(sc, 4 * c + i), s_, acc[c][i]);
+          }
+        }
+      };
+      for (uint32_t s0 = (uint32_t) wave; s0 < nblk; s0 += 2 * L) {
+        round(s0, sa, sb2);
+        if (s0 + L >= nblk) break;
+        round(s0 + L, sb2, sa);
+      }
     }
     // the tree's levels L/2 .. W within the wave: chains c and c + o (logical lanes ll and ll ^ W o)
 #pragma unroll
@@ -608,7 +693,7 @@ __global__ __launch_bounds__(W * kWave) void kernel16(const uint8_t* const* __re
 template <uint32_t T, int L, int G, int W>
 bool launch(const void* const* w, const int32_t* cnt, const int32_t* xrow, uint32_t n_mat, uint32_t rows,
             uint32_t cols, const int8_t* q, const float* d, float* y, uint32_t ys, hipStream_t s) {
-  const Lds<G, W> l((uint32_t) row_bytes<T>(cols), grid_bytes_of<T>());
+  const Lds<G, W, G == 1 && stage_a<T, L>() ? L : 0> l((uint32_t) row_bytes<T>(cols), grid_bytes_of<T>());
   if (l.total > 160 * 1024) return false;
   auto pick = [&]() {
     if constexpr (G == 1) return (cols / 32) % L == 0 ? kernel16<T, L, W, true> : kernel16<T, L, W, false>;
