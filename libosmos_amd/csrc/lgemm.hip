@@ -526,11 +526,94 @@ void kernel16(const uint8_t* const* __restrict__ w,
       if (tk < n) y[(uint64_t) (r0 + tk) * ys + row0 + col] = tv[0];
     }
   };
+  auto pass8s = [&](uint32_t c0) __attribute__((always_inline)) {
+    const bool lives = (col % 2 == 0) == (quad < 2);
+    const uint32_t t = c0 + col / 2, to = c0 + 2 * quad + (col & 1);
+    (void) t;
+    const uint32_t xoff = to < n ? to * nblk * 4 : 0x80000000u;
+    const uint32_t kc8 = (uint32_t) (col / 2) < (uint32_t) C ? (uint32_t) (col / 2) : (uint32_t) (C - 1);
+    float acc[C][2];
+#pragma unroll
+    for (int c = 0; c < C; c++) acc[c][0] = acc[c][1] = 0.0f;
+    // the round's A rows (8 tokens x L blocks x 32 bytes: one 16-byte word a thread) staged in LDS as in the 16-token
+    // pass; lane l reads its token's 8 bytes there where its half lives, zeros elsewhere
+    constexpr uint32_t kAS = 32 * L + 16;
+    static_assert(C != 4 || 16 * L == kThreads, "one word a thread");
+    uint8_t* abuf = smem + L_.part;
+    const uint32_t tk = threadIdx.x / (2 * L), o16 = threadIdx.x % (2 * L);
+    const uint32_t gof = c0 + tk < n ? (c0 + tk) * cols + o16 * 16 : 0x80000000u, lof = tk * kAS + o16 * 16;
+    u32x4 st;
+    auto gstage = [&](uint32_t b0) __attribute__((always_inline)) {
+      st = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, gof, b0 * 32, 0));
+    };
+    const uint32_t nr = (nblk + L - 1) / L;
+    gstage(0);
+    auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
+      const uint32_t sb = s0 + W * kc8 < nblk ? s0 + W * kc8 : nblk - 1;
+      return __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(dr, xoff == 0x80000000u ? xoff : xoff + sb * 4, 0, 0));
+    };
+    float sa = sload((uint32_t) wave), sb2;
+    auto round = [&](uint32_t r, float& sc, float& nx_sc) __attribute__((always_inline)) {
+      __syncthreads();  // (the round before read by every wave)
+      *(u32x4*) (abuf + lof) = st;
+      __syncthreads();
+      gstage(r + 1 < nr ? (r + 1) * L : r * L);
+      const uint32_t s0 = r * L + wave;
+      nx_sc = sload(s0 + L < nblk ? s0 + L : s0);
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const uint32_t s = s0 + W * c;
+        if (!FULL && s >= nblk) break;  // (uniform)
+        const uint8_t* blk = brow + (s / per) * Block<T>::bytes;
+        const int j = (int) (s % per);
+        uint32_t w0, w1;
+        chunk<T>((lbytes) blk, j, quad, grid, sm, w0, w1);
+        const long b = (long) (((uint64_t) w1 << 32) | w0);
+        float f0, f1;
+        factors<T>((lbytes) blk, j, f0, f1);
+        const float n0 = -__fmul_rn(f0, kBiasF), n1 = -__fmul_rn(f1, kBiasF);
+        const long av = *(const long*) (abuf + (col / 2) * kAS + (wave + W * c) * 32 + 8 * quad);
+        const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(lives ? av : 0, b, bias, 0, 0, 0);
+        const float s0_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[0]), n0), __builtin_fmaf(f1, __int_as_float(D[1]), n1));
+        const float s1_ = __fadd_rn(__builtin_fmaf(f0, __int_as_float(D[2]), n0), __builtin_fmaf(f1, __int_as_float(D[3]), n1));
+        acc[c][0] = __builtin_fmaf(row_bcast(sc, 2 * c), s0_, acc[c][0]);
+        acc[c][1] = __builtin_fmaf(row_bcast(sc, 2 * c + 1), s1_, acc[c][1]);
+      }
+    };
+    for (uint32_t r = 0; r < nr; r += 2) {  // (uniform: every wave meets every barrier)
+      round(r, sa, sb2);
+      if (r + 1 >= nr) break;
+      round(r + 1, sb2, sa);
+    }
+    __syncthreads();  // (the last round's A rows read: the partial trees go where they were)
+#pragma unroll
+    for (int o = C / 2; o > 0; o >>= 1)
+#pragma unroll
+      for (int c = 0; c < o; c++)
+#pragma unroll
+        for (int p = 0; p < 2; p++) acc[c][p] = __fadd_rn(acc[c][p], acc[c + o][p]);
+#pragma unroll
+    for (int p = 0; p < 2; p++) part[(wave * 2 + p) * kWave + lane] = acc[0][p];
+    __syncthreads();
+    for (int p = (int) wave; p < 2; p += W) {
+      float tv[W];
+#pragma unroll
+      for (int v = 0; v < W; v++) tv[v] = part[(v * 2 + p) * kWave + lane];
+#pragma unroll
+      for (int o = W / 2; o > 0; o >>= 1)
+#pragma unroll
+        for (int v = 0; v < o; v++) tv[v] = __fadd_rn(tv[v], tv[v + o]);
+      const uint32_t tk = c0 + 2 * quad + p;
+      if (tk < n) y[(uint64_t) (r0 + tk) * ys + row0 + col] = tv[0];
+    }
+  };
   for (uint32_t c0 = 0; c0 < n; c0 += TOK) {
     __syncthreads();  // (the slab's first pass; then the last pass's partial trees read before they are rewritten)
     if constexpr (kPass8) {
       if (n - c0 <= 8) {  // (uniform)
-        pass8(c0);
+        if constexpr (kStageA && C == 4 && L == 32) pass8s(c0);  // (staged: IQ2_XXS 951-980 -> 932-967 us; slower at 16)
+        else pass8(c0);
         continue;
       }
     }
