@@ -200,7 +200,9 @@ constexpr int kGroup = 8;
 // one without its A loads 890): kernel16 halves the A loads a full group issues. measured on config 5's routing (512
 // tokens, 250 experts, the busiest 441), us, 2048 x 7168 / 7168 x 2048: kernel16 (W 8 / 4) IQ2_XXS 1098 / 1201,
 // IQ1_S 1133 / 1283, IQ2_XS 1136 / 1260, IQ2_S 1399 / 1434, IQ3_XXS 1260 (W 16; 1326 at 8) / 1421, and with the
-// last pass of at most 8 tokens in the 8-token layout 1055 / 1189, 1064 / 1232, 1082 / 1217, 1340 / -, 1218 / 1376;
+// last pass of at most 8 tokens in the 8-token layout 1055 / 1189, 1064 / 1232, 1082 / 1217, 1340 / -, 1218 / 1376,
+// and as built now (A rows staged where stage_a says, the scales' broadcast inside the fmac) 898 / 985, 1058 / 1145,
+// 1076 / 1024, 1329 / 1422, 1215 / 1308;
 // kernel with one group
 // of 8 a pass 1161 / 1223, 1188 / 1325, 1214 / 1254, 1583 / 1497, 1612 / 1508 (it was 1308 / 1362 for IQ2_XXS before
 // its loads were reworked); with two groups 1344 / 1360, 1347 / 1509, 1368 / 1386, 1709 / 1501, 1411 (W 16) / 1747;
