@@ -288,7 +288,7 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
   // the A operand's rows from a buffer descriptor over the matrix's token rows: a lane whose (row, k) is a zero of
   // the layout, or whose token is past the count, reads at an offset past the descriptor's end - zeros, no access
   const __amdgpu_buffer_rsrc_t qr =
-      __builtin_amdgcn_make_buffer_rsrc((void*) (q + (uint64_t) r0 * cols), (short) 0, 0x7FFFFFFF, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void*) (q + (uint64_t) r0 * cols), (short) 0, (int) (n * cols), 0x00020000);
   // and the block scales of this lane's output tokens (a token past the count: zero, no access)
   const __amdgpu_buffer_rsrc_t dr =
       __builtin_amdgcn_make_buffer_rsrc((void*) (d + (uint64_t) r0 * nblk), (short) 0, 0x7FFFFFFF, 0x00020000);
@@ -444,8 +444,11 @@ void kernel16(const uint8_t* const* __restrict__ w,
   const uint64_t* sm = (const uint64_t*) (smem + L_.sm);
   float* part = (float*) (smem + L_.part);  // [wave][pair][lane]: two outputs a lane at a time
   const uint8_t* brow = smem + L_.slab + col * rb;  // this lane's B row (a weight row)
+  // (the A rows' range the matrix's own n rows: a staged round's 16-byte words past a row's end - cols not a whole
+  // number of rounds - read the next token's bytes, unused, or zeros past the last row; their offset is all in the
+  // vector offset, which the range check covers)
   const __amdgpu_buffer_rsrc_t qr =
-      __builtin_amdgcn_make_buffer_rsrc((void*) (q + (uint64_t) r0 * cols), (short) 0, 0x7FFFFFFF, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void*) (q + (uint64_t) r0 * cols), (short) 0, (int) (n * cols), 0x00020000);
   const __amdgpu_buffer_rsrc_t dr =
       __builtin_amdgcn_make_buffer_rsrc((void*) (d + (uint64_t) r0 * nblk), (short) 0, 0x7FFFFFFF, 0x00020000);
   const uint32_t kc = (uint32_t) (col / 4) < (uint32_t) C ? (uint32_t) (col / 4) : (uint32_t) (C - 1);
@@ -547,7 +550,7 @@ void kernel16(const uint8_t* const* __restrict__ w,
     const uint32_t gof = c0 + tk < n ? (c0 + tk) * cols + o16 * 16 : 0x80000000u, lof = tk * kAS + o16 * 16;
     u32x4 st;
     auto gstage = [&](uint32_t b0) __attribute__((always_inline)) {
-      st = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, gof, b0 * 32, 0));
+      st = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, gof + b0 * 32, 0, 0));
     };
     const uint32_t nr = (nblk + L - 1) / L;
     gstage(0);
@@ -645,7 +648,7 @@ void kernel16(const uint8_t* const* __restrict__ w,
       auto gstage = [&](uint32_t b0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < PW; u++)
-          st[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, gof[u], b0 * 32, 0));
+          st[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, gof[u] + b0 * 32, 0, 0));
       };
       auto sload = [&](uint32_t s0) __attribute__((always_inline)) {
         const uint32_t sb = s0 + W * kc < nblk ? s0 + W * kc : nblk - 1;  // (per lane: a vector offset)

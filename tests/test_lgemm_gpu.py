@@ -31,7 +31,7 @@ def run(g, t, ws, counts, rows, cols, q, d):
     return g.host(y), xrow
 
 
-@pytest.mark.parametrize("cols", [512, 4096])
+@pytest.mark.parametrize("cols", [512, 768, 4096, 4352])  # (768, 4352: a short last round of blocks)
 @pytest.mark.parametrize("name", LG_TYPES)
 def test_lane_group_oracle(g, name, cols):
     t = synth.ID[name]
