@@ -412,8 +412,10 @@ __global__ __launch_bounds__(W * kWave) void kernel(const uint8_t* const* __rest
 // a matrix's last pass with at most 8 tokens takes the 8-token layout instead (pass8: one MFMA a block, 2 outputs a
 // lane, all live; config 5's IQ2_XXS gate 1095-1119 -> 1049-1072 us, the same bits)
 template <uint32_t T, int L, int W, bool FULL>
-// (IQ2_XXS at 32 lanes with whole rounds held to 80 VGPRs, 6 waves a SIMD: 1078 -> 953 us, 7 registers spilled)
-__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(T == kIQ2_XXS && L == 32 && FULL ? 6 : 1)))
+// (IQ2_XXS at 32 lanes with whole rounds held to 80 VGPRs, 6 waves a SIMD: 1078 -> 953 us, 7 registers spilled; a
+// 16-wave workgroup held to 64, two workgroups a CU - IQ3_XXS at 32 lanes ran 1613 against 1215 us at 65)
+__global__ __launch_bounds__(W * kWave)
+__attribute__((amdgpu_waves_per_eu(T == kIQ2_XXS && L == 32 && FULL ? 6 : W == 16 ? 8 : 1)))
 void kernel16(const uint8_t* const* __restrict__ w,
                                                      const int32_t* __restrict__ cnt, const int32_t* __restrict__ xrow,
                                                      uint32_t cols, const int8_t* __restrict__ q,
