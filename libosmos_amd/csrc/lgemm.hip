@@ -177,11 +177,13 @@ constexpr int kBias = 0x4B400000;
 
 // acc + v(lane n of the lane's 16-lane row) x x, one rounding: the contract's chain step with its token scale taken
 // by DPP row_newbcast in the same instruction (v_fmac_f32 with a DPP source: no separate broadcast move; config 5's
-// IQ2_XXS gate 921-936 -> 898 us, every type 0-3 % faster; n a compile-time constant once unrolled)
+// IQ2_XXS gate 921-936 -> 898 us, every type 0-3 % faster; n a compile-time constant once unrolled). a DPP read of a
+// VGPR that a VALU instruction wrote in the two before needs two wait states, and the compiler's hazard pass does not
+// look inside the asm, so the asm brings its own (s_nop 1: 0.5-0.8 % of the kernel)
 __device__ inline float fmac_bcast(float acc, float v, float x, int n) {
   switch (n) {
 #define B(i) \
-  case i: asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:" #i " row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(v), "v"(x)); break;
+  case i: asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:" #i " row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(v), "v"(x)); break;
     B(0) B(1) B(2) B(3) B(4) B(5) B(6) B(7) B(8) B(9) B(10) B(11) B(12) B(13) B(14) B(15)
 #undef B
   }
